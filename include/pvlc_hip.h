@@ -1,0 +1,388 @@
+/*
+ * pvlc_hip — MI355X (gfx950) backend for the PaddleOCR-VL decoder KV-cache hot
+ * path: KV append with rotary, GQA decode attention and causal prefill.
+ *
+ * C ABI.  Plain pointers and sizes; no C++ or framework types.  Every entry
+ * point below names the reference interface it replaces
+ * (glebkudr/paddleocr-vl-webgpu; paths relative to the repository root).
+ *
+ * Pinned topology (runtime-core lib.rs:1123-1131): 16 query heads, 2 key/value
+ * heads (contiguous groups of 8 query heads), head_dim 128.
+ *
+ * Status codes: 0 is success.  A failure packs the reference's
+ * RuntimeErrorCode (crates/pvlc-runtime-native/src/lib.rs:273-283) in bits
+ * 8..15 and, for plan failures, the InvocationErrorCode
+ * (crates/pvlc-runtime-core/src/lib.rs:5335-5351) in bits 0..7.  The message of
+ * the last failure on the calling thread is pvlc_hip_last_error_message().
+ *
+ * Two families of entry points:
+ *  - the reference surface (host f32 buffers, copied in and out, plan
+ *    validation before any GPU effect, persistent sessions that poison on a
+ *    failure after submission);
+ *  - the device-resident hot path (fp16 device buffers, caller stream, blocked
+ *    paged KV layout below), used for batched decode, the 18-layer decode step
+ *    and prefill.  These never synchronise and never allocate.
+ */
+#ifndef PVLC_HIP_H
+#define PVLC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t pvlc_hip_status;
+
+/* RuntimeErrorCode, native lib.rs:273-283 (bits 8..15 of a status). */
+enum {
+    PVLC_HIP_OK = 0,
+    PVLC_HIP_ADAPTER_UNAVAILABLE = 1,
+    PVLC_HIP_DEVICE_REQUEST = 2,
+    PVLC_HIP_INVALID_INVOCATION = 3,
+    PVLC_HIP_VALIDATION = 4,
+    PVLC_HIP_OUT_OF_MEMORY = 5,
+    PVLC_HIP_INTERNAL = 6,
+    PVLC_HIP_OPERATION = 7,
+    PVLC_HIP_MAPPING = 8,
+    PVLC_HIP_CAPTURE = 9
+};
+
+/* InvocationErrorCode, runtime-core lib.rs:5335-5351 (bits 0..7 of a status). */
+enum {
+    PVLC_HIP_INV_NONE = 0,
+    PVLC_HIP_INV_ZERO_DIMENSION = 1,
+    PVLC_HIP_INV_LENGTH_MISMATCH = 2,
+    PVLC_HIP_INV_ARITHMETIC_OVERFLOW = 3,
+    PVLC_HIP_INV_INVALID_EPSILON = 4,
+    PVLC_HIP_INV_INVALID_ROTARY_DIMENSION = 5,
+    PVLC_HIP_INV_INVALID_ROPE_BASE = 6,
+    PVLC_HIP_INV_UNSUPPORTED_HEAD_DIMENSION = 7,
+    PVLC_HIP_INV_INVALID_DECODER_GEOMETRY = 8,
+    PVLC_HIP_INV_INVALID_VISION_GEOMETRY = 9,
+    PVLC_HIP_INV_INVALID_PROJECTOR_GEOMETRY = 10,
+    PVLC_HIP_INV_INVALID_SEQUENCE_BOUNDARIES = 11,
+    PVLC_HIP_INV_INVALID_CHECKPOINT_SELECTION = 12,
+    PVLC_HIP_INV_INVALID_ACTIVATION_LAYOUT = 13,
+    PVLC_HIP_INV_INVALID_FUSION_TARGET = 14,
+    PVLC_HIP_INV_NON_FINITE_INPUT = 15
+};
+
+#define PVLC_HIP_QUERY_HEADS 16u
+#define PVLC_HIP_KV_HEADS 2u
+#define PVLC_HIP_HEAD_DIM 128u
+/* Tokens per KV block of the device layout. */
+#define PVLC_HIP_BLOCK_TOKENS 16u
+/* runtime-core PINNED_DECODER_GQA_SPLIT_CHUNK_SIZE / _PARTIAL_STRIDE_F32, lib.rs:2884-2887 */
+#define PVLC_HIP_REFERENCE_SPLIT_CHUNK 32u
+#define PVLC_HIP_REFERENCE_PARTIAL_STRIDE_F32 192u
+
+/* Message of the last failure on this thread ("" after a success). */
+const char *pvlc_hip_last_error_message(void);
+
+/* ---------------------------------------------------------------------------
+ * Plans (host only, no GPU): the runtime-core plan authority.
+ * ------------------------------------------------------------------------- */
+
+/* DecoderKvSessionDescriptor, runtime-core lib.rs:833-843.  The caches are the
+ * compact physical planes [cache_capacity, 2, 128]; only the first
+ * prefix_tokens rows are semantic (rows after them may hold poison). */
+typedef struct pvlc_hip_kv_session_descriptor {
+    uint32_t query_heads;
+    uint32_t key_value_heads;
+    uint32_t head_dim;
+    uint32_t prefix_tokens;
+    uint32_t cache_capacity;
+    const float *key_cache;
+    size_t key_cache_len;
+    const float *value_cache;
+    size_t value_cache_len;
+} pvlc_hip_kv_session_descriptor;
+
+/* DecoderKvSessionPlan, runtime-core lib.rs:853-870. */
+typedef struct pvlc_hip_kv_session_plan {
+    uint32_t initial_cache_tokens;
+    uint32_t cache_capacity;
+    uint32_t query_heads;
+    uint32_t key_value_heads;
+    uint32_t head_dim;
+    uint64_t query_elements;
+    uint64_t key_value_width;
+    uint64_t cache_elements;
+    uint64_t cache_bytes;
+    uint64_t attention_bytes;
+    uint64_t split_partials_bytes;
+} pvlc_hip_kv_session_plan;
+
+/* DecoderKvSessionStep, runtime-core lib.rs:845-851. */
+typedef struct pvlc_hip_kv_step_operands {
+    const float *query;
+    size_t query_len;
+    const float *appended_key;
+    size_t appended_key_len;
+    const float *appended_value;
+    size_t appended_value_len;
+} pvlc_hip_kv_step_operands;
+
+/* DecoderGqaSplitPlan, runtime-core lib.rs:2871-2881 (the reference split-K
+ * geometry; this backend's kernels use their own partition size, but the plan
+ * is kept so callers see the same admission rules). */
+typedef struct pvlc_hip_gqa_split_plan {
+    uint32_t chunk_size;
+    uint32_t chunk_count;
+    uint64_t partials_elements;
+    uint64_t partials_bytes;
+    uint32_t partial_stride_f32;
+    uint32_t partial_workgroups;
+    uint32_t merge_workgroups;
+    uint32_t uniform_words[4];
+} pvlc_hip_gqa_split_plan;
+
+/* DecoderKvSessionStepPlan, runtime-core lib.rs:872-881. */
+typedef struct pvlc_hip_kv_step_plan {
+    uint32_t cache_tokens_before;
+    uint32_t cache_tokens_after;
+    uint64_t valid_cache_elements;
+    uint32_t append_uniform_words[4];
+    uint32_t attention_uniform_words[4];
+    pvlc_hip_gqa_split_plan split_gqa;
+} pvlc_hip_kv_step_plan;
+
+/* DecoderKvSessionDescriptor::plan, runtime-core lib.rs:952-968. */
+pvlc_hip_status pvlc_hip_kv_session_plan_create(const pvlc_hip_kv_session_descriptor *descriptor,
+                                                pvlc_hip_kv_session_plan *plan_out);
+
+/* DecoderKvSessionPlan::plan_cache_transition / plan_step, runtime-core
+ * lib.rs:976-1054.  step may be NULL (transition only). */
+pvlc_hip_status pvlc_hip_kv_session_plan_step(const pvlc_hip_kv_session_plan *plan, uint32_t cache_tokens,
+                                              const pvlc_hip_kv_step_operands *step,
+                                              pvlc_hip_kv_step_plan *step_plan_out);
+
+/* DecoderGqaSplitDescriptor::plan, runtime-core lib.rs:2889-2978. */
+pvlc_hip_status pvlc_hip_gqa_split_plan_create(uint32_t cache_tokens, uint32_t query_heads,
+                                               uint32_t key_value_heads, uint32_t head_dim,
+                                               pvlc_hip_gqa_split_plan *plan_out);
+
+/* require_decoder_prefill_tokens, runtime-core lib.rs:2491-2498 (the token
+ * bound of DecoderStackGeometryDescriptor::plan_prefill, :2293-2297). */
+pvlc_hip_status pvlc_hip_prefill_plan_check(uint32_t tokens, uint32_t cache_capacity);
+
+/* ---------------------------------------------------------------------------
+ * Runtime and persistent KV sessions (pvlc-runtime-native surface).
+ * ------------------------------------------------------------------------- */
+
+typedef struct pvlc_hip_runtime pvlc_hip_runtime;
+typedef struct pvlc_hip_kv_session pvlc_hip_kv_session;
+
+/* NativeOptions, native lib.rs:268-271 (the observer is replaced by counters). */
+typedef struct pvlc_hip_runtime_options {
+    int32_t device; /* HIP device ordinal */
+} pvlc_hip_runtime_options;
+
+/* Per-runtime counters (RuntimeCounters, native lib.rs:134-145). */
+typedef struct pvlc_hip_runtime_counters {
+    uint64_t kernel_launches;
+    uint64_t host_to_device_copies;
+    uint64_t device_to_host_copies;
+    uint64_t synchronizations;
+    uint64_t sessions_created;
+} pvlc_hip_runtime_counters;
+
+/* NativeRuntime::new, native lib.rs:912-1018.  Fails with
+ * PVLC_HIP_ADAPTER_UNAVAILABLE when no gfx950 device is visible. */
+pvlc_hip_status pvlc_hip_runtime_create(const pvlc_hip_runtime_options *options, pvlc_hip_runtime **runtime_out);
+void pvlc_hip_runtime_destroy(pvlc_hip_runtime *runtime);
+pvlc_hip_status pvlc_hip_runtime_counters_get(const pvlc_hip_runtime *runtime, pvlc_hip_runtime_counters *out);
+
+/* DecoderCachedGqaInvocation, runtime-core lib.rs:883-900. */
+typedef struct pvlc_hip_cached_gqa_invocation {
+    uint32_t query_heads;
+    uint32_t key_value_heads;
+    uint32_t head_dim;
+    uint32_t prefix_tokens;
+    uint32_t cache_capacity;
+    const float *query;
+    size_t query_len;
+    const float *appended_key;
+    size_t appended_key_len;
+    const float *appended_value;
+    size_t appended_value_len;
+    const float *key_cache;
+    size_t key_cache_len;
+    const float *value_cache;
+    size_t value_cache_len;
+} pvlc_hip_cached_gqa_invocation;
+
+/* DecoderCachedGqaExecution, native lib.rs:519-526: caller-owned outputs. */
+typedef struct pvlc_hip_cached_gqa_execution {
+    float *attention; /* query_heads*head_dim */
+    size_t attention_len;
+    float *key_cache; /* cache_capacity*2*128: the physical planes after the append */
+    size_t key_cache_len;
+    float *value_cache;
+    size_t value_cache_len;
+    uint32_t cache_tokens;   /* out */
+    uint32_t cache_capacity; /* out */
+    uint64_t queue_wall_time_ns;
+} pvlc_hip_cached_gqa_execution;
+
+/* NativeRuntime::run_decoder_cached_gqa, native lib.rs:1259-1264 (one-shot:
+ * upload the cache, append, attend, read everything back). */
+pvlc_hip_status pvlc_hip_run_decoder_cached_gqa(pvlc_hip_runtime *runtime,
+                                                const pvlc_hip_cached_gqa_invocation *invocation,
+                                                pvlc_hip_cached_gqa_execution *execution);
+
+/* NativeRuntime::begin_decoder_kv_session, native lib.rs:1266-1271 and
+ * decoder_kv_session.rs:62-82.  Validation precedes every GPU effect. */
+pvlc_hip_status pvlc_hip_begin_decoder_kv_session(pvlc_hip_runtime *runtime,
+                                                  const pvlc_hip_kv_session_descriptor *descriptor,
+                                                  pvlc_hip_kv_session **session_out);
+
+/* NativeDecoderKvSession::cache_tokens / cache_capacity, decoder_kv_session.rs:486-496. */
+uint32_t pvlc_hip_kv_session_cache_tokens(const pvlc_hip_kv_session *session);
+uint32_t pvlc_hip_kv_session_cache_capacity(const pvlc_hip_kv_session *session);
+/* 1 while the session is terminally poisoned (decoder_kv_session.rs:18-21). */
+int32_t pvlc_hip_kv_session_is_poisoned(const pvlc_hip_kv_session *session);
+
+/* DecoderKvSessionStepExecution diagnostics, native lib.rs:566-594. */
+typedef struct pvlc_hip_kv_step_execution {
+    uint32_t cache_tokens_before;
+    uint32_t cache_tokens_after;
+    uint64_t queue_wall_time_ns;
+    uint32_t dispatch_count;
+} pvlc_hip_kv_step_execution;
+
+/* NativeDecoderKvSession::step, decoder_kv_session.rs:499-529: append the
+ * (already rotated) key/value row at cache_tokens, attend over cache_tokens+1
+ * rows, write query_heads*head_dim f32 to attention.  An invalid step has no
+ * effect; a failure after submission poisons the session terminally. */
+pvlc_hip_status pvlc_hip_kv_session_step(pvlc_hip_kv_session *session, const pvlc_hip_kv_step_operands *step,
+                                         float *attention, size_t attention_len,
+                                         pvlc_hip_kv_step_execution *execution_out);
+
+/* NativeDecoderKvSession::finish, decoder_kv_session.rs:531-545, :812-925:
+ * read the full physical planes back.  Consumes the session: it is freed
+ * whether or not the call succeeds, like Rust's `finish(self)`. */
+pvlc_hip_status pvlc_hip_kv_session_finish(pvlc_hip_kv_session *session, float *key_cache, size_t key_cache_len,
+                                           float *value_cache, size_t value_cache_len, uint32_t *cache_tokens_out,
+                                           uint32_t *cache_capacity_out);
+
+/* Drop without finishing (Rust's Drop of NativeDecoderKvSession). */
+void pvlc_hip_kv_session_destroy(pvlc_hip_kv_session *session);
+
+/* Fault injection for tests, standing in for the reference's panicking
+ * observer (decoder_kv_session_native_contract.rs:848-909): the next step
+ * fails after its GPU work is submitted, which poisons the session. */
+void pvlc_hip_kv_session_fail_next_step_after_submit(pvlc_hip_kv_session *session);
+
+/* ---------------------------------------------------------------------------
+ * Device-resident hot path (fp16, caller stream, no allocation, no sync).
+ *
+ * Blocked KV layout in HBM.  A cache is two planes of 16-token blocks:
+ *   key plane   [num_blocks][2 kv heads][16 dim-chunks][16 tokens][8 dims]
+ *   value plane [num_blocks][2 kv heads][128 dims][16 tokens]
+ * so key element (block b, head h, token t, dim d) is at
+ *   ((b*2 + h)*16 + d/8)*128 + t*8 + d%8
+ * and value element at ((b*2 + h)*128 + d)*16 + t (fp16 elements).  Each
+ * (block, head) is 4 KiB per plane.  The compact reference planes
+ * [tokens][2][128] convert to and from this layout bit-exactly with
+ * pvlc_hip_kv_pack_f16 / pvlc_hip_kv_unpack_f16.
+ *
+ * A "sequence" owns a row of a block table; contiguous caches (block_tables
+ * NULL) give sequence s the blocks s*max_blocks_per_seq + j, which is how the
+ * 18-layer decode step addresses one cache per layer.
+ * ------------------------------------------------------------------------- */
+
+/* cos/sin tables [rows][rotary_dim/2] f32 with angle(pos, i) =
+ * pos * base^(-(2i/rotary_dim)), computed exactly as apply_rope_neox
+ * (cpu-ref lib.rs:459-461) with the host libm.  Host only. */
+pvlc_hip_status pvlc_hip_rope_table_f32(float base, uint32_t rotary_dim, uint32_t rows, float *cos_out,
+                                        float *sin_out);
+
+/* IEEE binary16 round-to-nearest-even conversion on the host (the rounding the
+ * kernels apply to every value they store). */
+void pvlc_hip_f32_to_f16_host(const float *in, uint16_t *out, size_t n);
+void pvlc_hip_f16_to_f32_host(const uint16_t *in, float *out, size_t n);
+
+typedef struct pvlc_hip_paged_decode_args {
+    uint32_t num_seqs;           /* sequences (or layers of one step) in this launch */
+    uint32_t num_blocks;         /* blocks in each plane (bounds every block id) */
+    uint32_t max_blocks_per_seq; /* row stride of block_tables */
+    const int32_t *block_tables; /* [num_seqs][max_blocks_per_seq] or NULL (contiguous) */
+    const int32_t *cache_lens;   /* [num_seqs] rows already cached = append position, or NULL */
+    uint32_t uniform_cache_len;  /* used for every sequence when cache_lens is NULL */
+    uint32_t max_context;        /* >= cache_len+1 of every sequence (sizes the grid) */
+    uint16_t *key_cache;
+    uint16_t *value_cache;
+    const uint16_t *query;     /* [num_seqs][16][128] fp16 */
+    const uint16_t *new_key;   /* [num_seqs][2][128] fp16, rotated in-kernel when rope tables given */
+    const uint16_t *new_value; /* [num_seqs][2][128] fp16 */
+    uint16_t *out;             /* [num_seqs][16][128] fp16 */
+    const float *rope_cos;     /* [rope_rows][64] or NULL: no rotary */
+    const float *rope_sin;
+    uint32_t rope_rows;
+    const int32_t *positions; /* [num_seqs] rotary position of the new token, or NULL = cache_len */
+    uint32_t rotate_query;    /* also rotate the query at that position */
+    uint32_t partition_tokens; /* split-K partition (64..4096, multiple of 64); 0 = automatic */
+    void *workspace;           /* from pvlc_hip_paged_decode_workspace_bytes, initialised once */
+    size_t workspace_bytes;
+} pvlc_hip_paged_decode_args;
+
+/* Partition size the automatic choice (partition_tokens = 0) uses. */
+uint32_t pvlc_hip_paged_decode_partition(uint32_t num_seqs, uint32_t max_context);
+/* Workspace for split-K partials, merge counters and the device error word. */
+size_t pvlc_hip_paged_decode_workspace_bytes(uint32_t num_seqs, uint32_t max_context, uint32_t partition_tokens);
+/* Zero a workspace on `stream` (a fill kernel; safe under graph capture). */
+pvlc_hip_status pvlc_hip_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
+/* Device error word of a workspace (0 = no clamped access); synchronises. */
+pvlc_hip_status pvlc_hip_workspace_error(const void *workspace, size_t workspace_bytes, void *stream,
+                                         uint32_t *error_out);
+
+/* One decode step for every sequence: rotate the new key (and optionally the
+ * query), append the new K/V row at cache_len, then GQA attention over
+ * cache_len+1 rows with split-K partitions merged in-kernel by the last
+ * partition to finish (LSE merge).  Replaces the per-layer chain
+ * decoder_mrope_f32 -> decoder_kv_append_f32 -> decoder_gqa_split_partial_f32 ->
+ * decoder_gqa_split_merge_f32 (pvlc-wgsl lib.rs:927-952, 1024-1234; issued by
+ * pvlc-runtime-web decoder_stack_session.rs:4698-4729) with one launch. */
+pvlc_hip_status pvlc_hip_paged_decode_f16(const pvlc_hip_paged_decode_args *args, void *stream);
+
+typedef struct pvlc_hip_paged_prefill_args {
+    uint32_t tokens;            /* N */
+    uint32_t num_blocks;
+    const int32_t *block_table; /* [ceil(N/16)] or NULL = blocks 0.. */
+    uint16_t *key_cache;
+    uint16_t *value_cache;
+    const uint16_t *query; /* [N][16][128] fp16 */
+    const uint16_t *key;   /* [N][2][128] */
+    const uint16_t *value; /* [N][2][128] */
+    uint16_t *out;         /* [N][16][128] */
+    const float *rope_cos; /* [rope_rows][64] or NULL */
+    const float *rope_sin;
+    uint32_t rope_rows;
+    const int32_t *positions; /* [N] or NULL = 0..N-1 */
+    uint16_t *query_scratch;  /* [N][16][128] fp16: the rotated query */
+} pvlc_hip_paged_prefill_args;
+
+/* Causal prefill: rotary on Q and K, write all N K/V rows into the blocked
+ * cache, then MFMA causal GQA attention (fp16 in, f32 accumulate, fp16 out).
+ * Replaces decoder_prefill_mrope_f32 -> decoder_kv_append_range_f32 ->
+ * decoder_prefill_gqa_f32 (pvlc-wgsl lib.rs:1262-1416; issued by
+ * decoder_stack_session.rs:5044-5064). */
+pvlc_hip_status pvlc_hip_paged_prefill_f16(const pvlc_hip_paged_prefill_args *args, void *stream);
+
+/* Compact [tokens][2][128] fp16 rows <-> blocked planes (bit-exact), rows
+ * 0..tokens-1 of one sequence through its block table (NULL = blocks 0..). */
+pvlc_hip_status pvlc_hip_kv_pack_f16(const uint16_t *key_rows, const uint16_t *value_rows, uint32_t tokens,
+                                     const int32_t *block_table, uint32_t num_blocks, uint16_t *key_cache,
+                                     uint16_t *value_cache, void *stream);
+pvlc_hip_status pvlc_hip_kv_unpack_f16(const uint16_t *key_cache, const uint16_t *value_cache, uint32_t tokens,
+                                       const int32_t *block_table, uint32_t num_blocks, uint16_t *key_rows,
+                                       uint16_t *value_rows, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PVLC_HIP_H */

@@ -1,0 +1,84 @@
+// Internal declarations shared by the pvlc_hip translation units.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "pvlc_hip.h"
+
+namespace pvlc {
+
+constexpr uint32_t kQueryHeads = PVLC_HIP_QUERY_HEADS;
+constexpr uint32_t kKvHeads = PVLC_HIP_KV_HEADS;
+constexpr uint32_t kHeadDim = PVLC_HIP_HEAD_DIM;
+constexpr uint32_t kGroup = kQueryHeads / kKvHeads;
+constexpr uint32_t kBlockTokens = PVLC_HIP_BLOCK_TOKENS;
+constexpr uint32_t kRowElems = kKvHeads * kHeadDim;          // one cache row, both heads
+constexpr uint32_t kBlockHeadElems = kBlockTokens * kHeadDim;  // one (block, head) slab
+constexpr uint32_t kMaxDecoderHeadDim = 128;                   // runtime-core lib.rs:180
+constexpr uint32_t kMaxWebgpuDispatch = 65535;                 // runtime-core lib.rs:187
+
+// Status of a failed call: RuntimeErrorCode in bits 8..15, InvocationErrorCode
+// in bits 0..7; records the message for pvlc_hip_last_error_message().
+pvlc_hip_status fail(int runtime_code, int invocation_code, const std::string &message);
+inline pvlc_hip_status invalid(int invocation_code, const std::string &message) {
+    return fail(PVLC_HIP_INVALID_INVOCATION, invocation_code, message);
+}
+pvlc_hip_status ok();
+
+// Plan-layer error: an InvocationErrorCode plus message (runtime-core's
+// InvocationError, lib.rs:5365-5395).
+struct PlanError {
+    int code = PVLC_HIP_INV_NONE;
+    std::string message;
+    explicit operator bool() const { return code != PVLC_HIP_INV_NONE; }
+};
+
+PlanError plan_session_geometry(uint32_t query_heads, uint32_t key_value_heads, uint32_t head_dim,
+                                uint32_t prefix_tokens, uint32_t cache_capacity, pvlc_hip_kv_session_plan *out);
+PlanError plan_split(uint32_t cache_tokens, uint32_t query_heads, uint32_t key_value_heads, uint32_t head_dim,
+                     pvlc_hip_gqa_split_plan *out);
+PlanError plan_descriptor(const pvlc_hip_kv_session_descriptor *d, pvlc_hip_kv_session_plan *out);
+PlanError plan_step(const pvlc_hip_kv_session_plan *plan, uint32_t cache_tokens, const pvlc_hip_kv_step_operands *step,
+                    pvlc_hip_kv_step_plan *out);
+PlanError plan_cached_gqa(const pvlc_hip_cached_gqa_invocation *inv, pvlc_hip_kv_session_plan *session_out,
+                          pvlc_hip_kv_step_plan *step_out);
+
+// fp16 storage admits only values whose RNE rounding is finite (|x| < 65520).
+bool fp16_representable(const float *values, size_t n);
+uint16_t f32_to_f16_rne(float value);
+float f16_to_f32(uint16_t bits);
+
+// Host copies between the compact reference rows [tokens][2][128] and the
+// blocked device layout (contiguous blocks 0..ceil(tokens/16)-1).
+size_t key_blocked_index(uint32_t token, uint32_t head, uint32_t dim);
+size_t value_blocked_index(uint32_t token, uint32_t head, uint32_t dim);
+
+// Kernel launchers (kernels_*.hip).  Return hipError_t as int.
+struct DecodeLaunch {
+    const pvlc_hip_paged_decode_args *args;
+    uint32_t partition_tokens;
+    uint32_t max_parts;
+    float *part_o;
+    float *part_ml;
+    uint32_t *counters;
+    uint32_t *error_word;
+};
+int launch_paged_decode(const DecodeLaunch &launch, void *stream);
+int launch_fill_u32(uint32_t *dst, size_t words, uint32_t value, void *stream);
+int launch_kv_pack(const uint16_t *key_rows, const uint16_t *value_rows, uint32_t tokens, const int32_t *table,
+                   uint32_t num_blocks, uint16_t *key_cache, uint16_t *value_cache, uint32_t *error_word,
+                   void *stream);
+int launch_kv_unpack(const uint16_t *key_cache, const uint16_t *value_cache, uint32_t tokens, const int32_t *table,
+                     uint32_t num_blocks, uint16_t *key_rows, uint16_t *value_rows, void *stream);
+int launch_prefill(const pvlc_hip_paged_prefill_args *args, void *stream);
+
+// Workspace layout of the paged decode.
+struct DecodeWorkspace {
+    size_t part_o_offset, part_ml_offset, counters_offset, error_offset, total;
+};
+DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts);
+uint32_t auto_partition(uint32_t num_seqs, uint32_t max_context);
+
+}  // namespace pvlc

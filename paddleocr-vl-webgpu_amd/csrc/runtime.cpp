@@ -1,0 +1,533 @@
+// Host runtime: the NativeRuntime / NativeDecoderKvSession surface of
+// crates/pvlc-runtime-native (glebkudr/paddleocr-vl-webgpu) on HIP, plus host
+// validation of the device-resident entry points.
+//
+// Contract kept from the reference:
+//  - every plan check runs before any GPU effect (decoder_kv_session.rs:62-82,
+//    :499-512), so an invalid step changes nothing;
+//  - a step marks the session Poisoned before submitting and restores Healthy
+//    only on success (:513-528); a poisoned session refuses step and finish;
+//  - one execution lock per runtime serialises GPU work (lib.rs:739);
+//  - cache planes cross the boundary in the compact [capacity][2][128] layout.
+// Storage is fp16: f32 operands are rounded to nearest even on the way in and
+// widened exactly on the way out; a finite f32 whose fp16 rounding overflows is
+// rejected as NonFiniteInput before any GPU effect.
+
+#include <hip/hip_runtime_api.h>
+
+#include <chrono>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "pvlc_internal.hpp"
+
+using namespace pvlc;
+
+struct pvlc_hip_runtime {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::mutex execution_lock;
+    pvlc_hip_runtime_counters counters{};
+};
+
+struct pvlc_hip_kv_session {
+    pvlc_hip_runtime *runtime = nullptr;
+    pvlc_hip_kv_session_plan plan{};
+    uint32_t cache_tokens = 0;
+    bool poisoned = false;
+    bool fail_next_after_submit = false;
+    uint32_t num_blocks = 0;
+    uint16_t *key_cache = nullptr;    // blocked planes
+    uint16_t *value_cache = nullptr;
+    uint16_t *step_operands = nullptr;  // device: query | key | value (fp16)
+    uint16_t *attention = nullptr;      // device: 16*128 fp16
+    void *workspace = nullptr;
+    size_t workspace_bytes = 0;
+    uint32_t partition = 0;
+    uint32_t max_parts = 0;
+    uint16_t *host_staging = nullptr;  // pinned: operands in, attention out
+};
+
+namespace {
+
+constexpr size_t kQueryElems = kQueryHeads * kHeadDim;
+constexpr size_t kStepElems = kQueryElems + 2 * kRowElems;
+
+pvlc_hip_status hip_fail(hipError_t e, const char *what) {
+    const int code = e == hipErrorOutOfMemory ? PVLC_HIP_OUT_OF_MEMORY : PVLC_HIP_OPERATION;
+    return fail(code, PVLC_HIP_INV_NONE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                            \
+    do {                                               \
+        hipError_t e_ = (expr);                        \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+uint64_t now_ns() {
+    return static_cast<uint64_t>(
+        std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch())
+            .count());
+}
+
+void free_session_buffers(pvlc_hip_kv_session *s) {
+    if (!s) return;
+    if (s->runtime) (void)hipSetDevice(s->runtime->device);
+    (void)hipFree(s->key_cache);
+    (void)hipFree(s->value_cache);
+    (void)hipFree(s->step_operands);
+    (void)hipFree(s->attention);
+    (void)hipFree(s->workspace);
+    (void)hipHostFree(s->host_staging);
+    s->key_cache = s->value_cache = s->step_operands = s->attention = nullptr;
+    s->workspace = nullptr;
+    s->host_staging = nullptr;
+}
+
+// Device-resident argument validation shared by the public entry point and the
+// session path.  Returns a status (0 = ok) without touching the GPU.
+pvlc_hip_status validate_decode_args(const pvlc_hip_paged_decode_args *a, uint32_t *partition_out,
+                                     uint32_t *max_parts_out, DecodeWorkspace *layout_out) {
+    if (!a) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "paged decode args are NULL");
+    if (a->num_seqs == 0 || a->num_blocks == 0 || a->max_blocks_per_seq == 0 || a->max_context == 0)
+        return invalid(PVLC_HIP_INV_ZERO_DIMENSION, "all paged decode dimensions must be nonzero");
+    if (!a->key_cache || !a->value_cache || !a->query || !a->new_key || !a->new_value || !a->out || !a->workspace)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "paged decode buffer pointer is NULL");
+    if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr) || (a->rope_cos && a->rope_rows == 0))
+        return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION, "rotary tables must be given together with rows");
+    if (!a->block_tables &&
+        static_cast<uint64_t>(a->num_seqs) * a->max_blocks_per_seq > static_cast<uint64_t>(a->num_blocks))
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY,
+                       "contiguous caches need num_seqs * max_blocks_per_seq blocks");
+    if (static_cast<uint64_t>(a->max_context) > static_cast<uint64_t>(a->max_blocks_per_seq) * kBlockTokens)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "max_context exceeds the block table span");
+    if (!a->cache_lens && a->uniform_cache_len + 1ull > a->max_context)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "uniform cache length leaves no append row");
+    if (a->num_seqs > 65535u) return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "num_seqs exceeds 65535");
+    uint32_t partition = a->partition_tokens ? a->partition_tokens : auto_partition(a->num_seqs, a->max_context);
+    if (partition < 64 || partition > 4096 || partition % 64 != 0)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "partition_tokens must be a multiple of 64 in 64..4096");
+    const uint32_t max_parts = (a->max_context + partition - 1) / partition;
+    const DecodeWorkspace layout = decode_workspace_layout(a->num_seqs, max_parts);
+    if (a->workspace_bytes < layout.total)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "workspace holds " + std::to_string(a->workspace_bytes) +
+                                                         " bytes but the launch needs " + std::to_string(layout.total));
+    if (partition_out) *partition_out = partition;
+    if (max_parts_out) *max_parts_out = max_parts;
+    if (layout_out) *layout_out = layout;
+    return PVLC_HIP_OK;
+}
+
+pvlc_hip_status launch_decode_checked(const pvlc_hip_paged_decode_args *a, void *stream) {
+    uint32_t partition = 0, max_parts = 0;
+    DecodeWorkspace layout{};
+    if (pvlc_hip_status st = validate_decode_args(a, &partition, &max_parts, &layout)) return st;
+    char *ws = static_cast<char *>(a->workspace);
+    DecodeLaunch launch{a,
+                        partition,
+                        max_parts,
+                        reinterpret_cast<float *>(ws + layout.part_o_offset),
+                        reinterpret_cast<float *>(ws + layout.part_ml_offset),
+                        reinterpret_cast<uint32_t *>(ws + layout.counters_offset),
+                        reinterpret_cast<uint32_t *>(ws + layout.error_offset)};
+    const int e = launch_paged_decode(launch, stream);
+    if (e != 0) return hip_fail(static_cast<hipError_t>(e), "paged decode launch");
+    return PVLC_HIP_OK;
+}
+
+// Session creation shared by begin_decoder_kv_session and the one-shot path.
+// The plan is already validated.
+pvlc_hip_status create_session(pvlc_hip_runtime *rt, const pvlc_hip_kv_session_plan &plan, const float *key_cache,
+                               const float *value_cache, pvlc_hip_kv_session **out) {
+    auto *s = new (std::nothrow) pvlc_hip_kv_session();
+    if (!s) return fail(PVLC_HIP_OUT_OF_MEMORY, PVLC_HIP_INV_NONE, "session allocation failed");
+    s->runtime = rt;
+    s->plan = plan;
+    s->cache_tokens = plan.initial_cache_tokens;
+    s->num_blocks = (plan.cache_capacity + kBlockTokens - 1) / kBlockTokens;
+    s->partition = auto_partition(1, plan.cache_capacity);
+    s->max_parts = (plan.cache_capacity + s->partition - 1) / s->partition;
+    s->workspace_bytes = decode_workspace_layout(1, s->max_parts).total;
+    const size_t plane_elems = static_cast<size_t>(s->num_blocks) * kBlockTokens * kRowElems;
+
+    auto cleanup = [&](pvlc_hip_status st) {
+        free_session_buffers(s);
+        delete s;
+        return st;
+    };
+    hipError_t e;
+    if ((e = hipSetDevice(rt->device)) != hipSuccess) return cleanup(hip_fail(e, "hipSetDevice"));
+    if ((e = hipMalloc(&s->key_cache, plane_elems * 2)) != hipSuccess) return cleanup(hip_fail(e, "key cache"));
+    if ((e = hipMalloc(&s->value_cache, plane_elems * 2)) != hipSuccess) return cleanup(hip_fail(e, "value cache"));
+    if ((e = hipMalloc(&s->step_operands, kStepElems * 2)) != hipSuccess) return cleanup(hip_fail(e, "operands"));
+    if ((e = hipMalloc(&s->attention, kQueryElems * 2)) != hipSuccess) return cleanup(hip_fail(e, "attention"));
+    if ((e = hipMalloc(&s->workspace, s->workspace_bytes)) != hipSuccess) return cleanup(hip_fail(e, "workspace"));
+    if ((e = hipHostMalloc(reinterpret_cast<void **>(&s->host_staging), (kStepElems + kQueryElems) * 2,
+                           hipHostMallocDefault)) != hipSuccess)
+        return cleanup(hip_fail(e, "pinned staging"));
+
+    // Initial planes: round to fp16 and scatter into the blocked layout on the
+    // host (rows past the capacity stay zero), then one copy per plane.
+    std::vector<uint16_t> kb(plane_elems, 0), vb(plane_elems, 0);
+    for (uint32_t t = 0; t < plan.cache_capacity; ++t) {
+        for (uint32_t h = 0; h < kKvHeads; ++h) {
+            for (uint32_t d = 0; d < kHeadDim; ++d) {
+                const size_t src = (static_cast<size_t>(t) * kKvHeads + h) * kHeadDim + d;
+                kb[key_blocked_index(t, h, d)] = f32_to_f16_rne(key_cache[src]);
+                vb[value_blocked_index(t, h, d)] = f32_to_f16_rne(value_cache[src]);
+            }
+        }
+    }
+    hipStream_t st = rt->stream;
+    if ((e = hipMemcpyAsync(s->key_cache, kb.data(), plane_elems * 2, hipMemcpyHostToDevice, st)) != hipSuccess)
+        return cleanup(hip_fail(e, "key cache upload"));
+    if ((e = hipMemcpyAsync(s->value_cache, vb.data(), plane_elems * 2, hipMemcpyHostToDevice, st)) != hipSuccess)
+        return cleanup(hip_fail(e, "value cache upload"));
+    const int fe = launch_fill_u32(static_cast<uint32_t *>(s->workspace), s->workspace_bytes / 4, 0u, st);
+    if (fe != 0) return cleanup(hip_fail(static_cast<hipError_t>(fe), "workspace init"));
+    if ((e = hipStreamSynchronize(st)) != hipSuccess) return cleanup(hip_fail(e, "session creation"));
+    rt->counters.host_to_device_copies += 2;
+    rt->counters.kernel_launches += 1;
+    rt->counters.synchronizations += 1;
+    rt->counters.sessions_created += 1;
+    *out = s;
+    return PVLC_HIP_OK;
+}
+
+// One append + attention on the session's device state.  Caller holds the
+// execution lock and has validated the step.
+pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_operands *step, float *attention,
+                             pvlc_hip_kv_step_execution *exec) {
+    pvlc_hip_runtime *rt = s->runtime;
+    const uint64_t started = now_ns();
+    uint16_t *stage = s->host_staging;
+    pvlc_hip_f32_to_f16_host(step->query, stage, kQueryElems);
+    pvlc_hip_f32_to_f16_host(step->appended_key, stage + kQueryElems, kRowElems);
+    pvlc_hip_f32_to_f16_host(step->appended_value, stage + kQueryElems + kRowElems, kRowElems);
+    HIP_TRY(hipSetDevice(rt->device), "hipSetDevice");
+    HIP_TRY(hipMemcpyAsync(s->step_operands, stage, kStepElems * 2, hipMemcpyHostToDevice, rt->stream),
+            "step operand upload");
+    rt->counters.host_to_device_copies += 1;
+
+    pvlc_hip_paged_decode_args a{};
+    a.num_seqs = 1;
+    a.num_blocks = s->num_blocks;
+    a.max_blocks_per_seq = s->num_blocks;
+    a.block_tables = nullptr;
+    a.cache_lens = nullptr;
+    a.uniform_cache_len = s->cache_tokens;
+    a.max_context = s->plan.cache_capacity;
+    a.key_cache = s->key_cache;
+    a.value_cache = s->value_cache;
+    a.query = s->step_operands;
+    a.new_key = s->step_operands + kQueryElems;
+    a.new_value = s->step_operands + kQueryElems + kRowElems;
+    a.out = s->attention;
+    a.partition_tokens = s->partition;
+    a.workspace = s->workspace;
+    a.workspace_bytes = s->workspace_bytes;
+    if (pvlc_hip_status st = launch_decode_checked(&a, rt->stream)) return st;
+    rt->counters.kernel_launches += 1;
+
+    uint16_t *result = stage + kStepElems;
+    HIP_TRY(hipMemcpyAsync(result, s->attention, kQueryElems * 2, hipMemcpyDeviceToHost, rt->stream),
+            "attention readback");
+    rt->counters.device_to_host_copies += 1;
+    HIP_TRY(hipStreamSynchronize(rt->stream), "decoder KV session step");
+    rt->counters.synchronizations += 1;
+    if (s->fail_next_after_submit) {
+        s->fail_next_after_submit = false;
+        return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE, "decoder KV session step: injected failure after submission");
+    }
+    pvlc_hip_f16_to_f32_host(result, attention, kQueryElems);
+    if (exec) {
+        exec->cache_tokens_before = s->cache_tokens;
+        exec->cache_tokens_after = s->cache_tokens + 1;
+        exec->queue_wall_time_ns = now_ns() - started;
+        exec->dispatch_count = 1;
+    }
+    return PVLC_HIP_OK;
+}
+
+// Copy the planes back to the compact f32 layout (rows 0..capacity-1).
+pvlc_hip_status read_planes(pvlc_hip_kv_session *s, float *key_out, float *value_out) {
+    pvlc_hip_runtime *rt = s->runtime;
+    const size_t plane_elems = static_cast<size_t>(s->num_blocks) * kBlockTokens * kRowElems;
+    std::vector<uint16_t> kb(plane_elems), vb(plane_elems);
+    HIP_TRY(hipSetDevice(rt->device), "hipSetDevice");
+    HIP_TRY(hipMemcpyAsync(kb.data(), s->key_cache, plane_elems * 2, hipMemcpyDeviceToHost, rt->stream),
+            "key cache readback");
+    HIP_TRY(hipMemcpyAsync(vb.data(), s->value_cache, plane_elems * 2, hipMemcpyDeviceToHost, rt->stream),
+            "value cache readback");
+    HIP_TRY(hipStreamSynchronize(rt->stream), "decoder KV session finish");
+    rt->counters.device_to_host_copies += 2;
+    rt->counters.synchronizations += 1;
+    for (uint32_t t = 0; t < s->plan.cache_capacity; ++t) {
+        for (uint32_t h = 0; h < kKvHeads; ++h) {
+            for (uint32_t d = 0; d < kHeadDim; ++d) {
+                const size_t dst = (static_cast<size_t>(t) * kKvHeads + h) * kHeadDim + d;
+                key_out[dst] = f16_to_f32(kb[key_blocked_index(t, h, d)]);
+                value_out[dst] = f16_to_f32(vb[value_blocked_index(t, h, d)]);
+            }
+        }
+    }
+    return PVLC_HIP_OK;
+}
+
+pvlc_hip_status check_fp16_range(const float *v, size_t n, const char *what) {
+    if (!fp16_representable(v, n))
+        return invalid(PVLC_HIP_INV_NON_FINITE_INPUT, std::string(what) + " holds a value outside the fp16 range");
+    return PVLC_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+pvlc_hip_status pvlc_hip_runtime_create(const pvlc_hip_runtime_options *options, pvlc_hip_runtime **runtime_out) {
+    if (!runtime_out) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "runtime_out is NULL");
+    *runtime_out = nullptr;
+    const int device = options ? options->device : 0;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fail(PVLC_HIP_ADAPTER_UNAVAILABLE, PVLC_HIP_INV_NONE, "no HIP device is visible");
+    if (device < 0 || device >= count)
+        return fail(PVLC_HIP_ADAPTER_UNAVAILABLE, PVLC_HIP_INV_NONE, "device ordinal out of range");
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+        return fail(PVLC_HIP_DEVICE_REQUEST, PVLC_HIP_INV_NONE, "device properties unavailable");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(PVLC_HIP_ADAPTER_UNAVAILABLE, PVLC_HIP_INV_NONE,
+                    std::string("pvlc_hip requires gfx950, found ") + prop.gcnArchName);
+    auto *rt = new (std::nothrow) pvlc_hip_runtime();
+    if (!rt) return fail(PVLC_HIP_OUT_OF_MEMORY, PVLC_HIP_INV_NONE, "runtime allocation failed");
+    rt->device = device;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete rt;
+        return fail(PVLC_HIP_DEVICE_REQUEST, PVLC_HIP_INV_NONE, std::string("stream creation: ") + hipGetErrorString(e));
+    }
+    *runtime_out = rt;
+    return ok();
+}
+
+void pvlc_hip_runtime_destroy(pvlc_hip_runtime *runtime) {
+    if (!runtime) return;
+    (void)hipSetDevice(runtime->device);
+    if (runtime->stream) (void)hipStreamDestroy(runtime->stream);
+    delete runtime;
+}
+
+pvlc_hip_status pvlc_hip_runtime_counters_get(const pvlc_hip_runtime *runtime, pvlc_hip_runtime_counters *out) {
+    if (!runtime || !out) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "NULL argument");
+    *out = runtime->counters;
+    return ok();
+}
+
+pvlc_hip_status pvlc_hip_begin_decoder_kv_session(pvlc_hip_runtime *runtime,
+                                                  const pvlc_hip_kv_session_descriptor *descriptor,
+                                                  pvlc_hip_kv_session **session_out) {
+    if (!runtime || !descriptor || !session_out) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "NULL argument");
+    *session_out = nullptr;
+    pvlc_hip_kv_session_plan plan{};
+    if (PlanError e = plan_descriptor(descriptor, &plan)) return invalid(e.code, e.message);
+    const size_t semantic = static_cast<size_t>(plan.initial_cache_tokens) * kRowElems;
+    if (pvlc_hip_status st = check_fp16_range(descriptor->key_cache, semantic, "key cache")) return st;
+    if (pvlc_hip_status st = check_fp16_range(descriptor->value_cache, semantic, "value cache")) return st;
+    std::lock_guard<std::mutex> guard(runtime->execution_lock);
+    pvlc_hip_status st = create_session(runtime, plan, descriptor->key_cache, descriptor->value_cache, session_out);
+    if (st != PVLC_HIP_OK) return fail(st >> 8, st & 0xff, std::string("decoder KV session creation: ") +
+                                                            pvlc_hip_last_error_message());
+    return ok();
+}
+
+uint32_t pvlc_hip_kv_session_cache_tokens(const pvlc_hip_kv_session *session) {
+    return session ? session->cache_tokens : 0;
+}
+
+uint32_t pvlc_hip_kv_session_cache_capacity(const pvlc_hip_kv_session *session) {
+    return session ? session->plan.cache_capacity : 0;
+}
+
+int32_t pvlc_hip_kv_session_is_poisoned(const pvlc_hip_kv_session *session) {
+    return session && session->poisoned ? 1 : 0;
+}
+
+void pvlc_hip_kv_session_fail_next_step_after_submit(pvlc_hip_kv_session *session) {
+    if (session) session->fail_next_after_submit = true;
+}
+
+pvlc_hip_status pvlc_hip_kv_session_step(pvlc_hip_kv_session *session, const pvlc_hip_kv_step_operands *step,
+                                         float *attention, size_t attention_len,
+                                         pvlc_hip_kv_step_execution *execution_out) {
+    if (!session || !step) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "NULL argument");
+    if (session->poisoned)
+        return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE, "decoder KV session is terminally poisoned");
+    pvlc_hip_kv_step_plan sp{};
+    if (PlanError e = plan_step(&session->plan, session->cache_tokens, step, &sp)) return invalid(e.code, e.message);
+    if (!attention || attention_len != kQueryElems)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "attention output must hold 2048 floats");
+    if (pvlc_hip_status st = check_fp16_range(step->query, step->query_len, "query")) return st;
+    if (pvlc_hip_status st = check_fp16_range(step->appended_key, step->appended_key_len, "appended key")) return st;
+    if (pvlc_hip_status st = check_fp16_range(step->appended_value, step->appended_value_len, "appended value"))
+        return st;
+    std::lock_guard<std::mutex> guard(session->runtime->execution_lock);
+    session->poisoned = true;
+    pvlc_hip_status st = execute_step(session, step, attention, execution_out);
+    if (st != PVLC_HIP_OK) return st;
+    session->cache_tokens = sp.cache_tokens_after;
+    session->poisoned = false;
+    return ok();
+}
+
+pvlc_hip_status pvlc_hip_kv_session_finish(pvlc_hip_kv_session *session, float *key_cache, size_t key_cache_len,
+                                           float *value_cache, size_t value_cache_len, uint32_t *cache_tokens_out,
+                                           uint32_t *cache_capacity_out) {
+    if (!session) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "session is NULL");
+    struct Consume {
+        pvlc_hip_kv_session *s;
+        ~Consume() {
+            free_session_buffers(s);
+            delete s;
+        }
+    } consume{session};
+    if (session->poisoned)
+        return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE, "decoder KV session is terminally poisoned");
+    if (!key_cache || !value_cache || key_cache_len != session->plan.cache_elements ||
+        value_cache_len != session->plan.cache_elements)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "finish outputs must hold cache_capacity*256 floats each");
+    std::lock_guard<std::mutex> guard(session->runtime->execution_lock);
+    if (pvlc_hip_status st = read_planes(session, key_cache, value_cache)) return st;
+    if (cache_tokens_out) *cache_tokens_out = session->cache_tokens;
+    if (cache_capacity_out) *cache_capacity_out = session->plan.cache_capacity;
+    return ok();
+}
+
+void pvlc_hip_kv_session_destroy(pvlc_hip_kv_session *session) {
+    if (!session) return;
+    free_session_buffers(session);
+    delete session;
+}
+
+pvlc_hip_status pvlc_hip_run_decoder_cached_gqa(pvlc_hip_runtime *runtime,
+                                                const pvlc_hip_cached_gqa_invocation *invocation,
+                                                pvlc_hip_cached_gqa_execution *execution) {
+    if (!runtime || !invocation || !execution) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "NULL argument");
+    pvlc_hip_kv_session_plan plan{};
+    pvlc_hip_kv_step_plan sp{};
+    if (PlanError e = plan_cached_gqa(invocation, &plan, &sp)) return invalid(e.code, e.message);
+    const size_t semantic = static_cast<size_t>(invocation->prefix_tokens) * kRowElems;
+    if (pvlc_hip_status st = check_fp16_range(invocation->key_cache, semantic, "key cache")) return st;
+    if (pvlc_hip_status st = check_fp16_range(invocation->value_cache, semantic, "value cache")) return st;
+    if (pvlc_hip_status st = check_fp16_range(invocation->query, invocation->query_len, "query")) return st;
+    if (pvlc_hip_status st = check_fp16_range(invocation->appended_key, kRowElems, "appended key")) return st;
+    if (pvlc_hip_status st = check_fp16_range(invocation->appended_value, kRowElems, "appended value")) return st;
+    if (!execution->attention || execution->attention_len != kQueryElems || !execution->key_cache ||
+        !execution->value_cache || execution->key_cache_len != plan.cache_elements ||
+        execution->value_cache_len != plan.cache_elements)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "execution outputs have the wrong lengths");
+    const uint64_t started = now_ns();
+    std::lock_guard<std::mutex> guard(runtime->execution_lock);
+    pvlc_hip_kv_session *s = nullptr;
+    if (pvlc_hip_status st = create_session(runtime, plan, invocation->key_cache, invocation->value_cache, &s))
+        return st;
+    pvlc_hip_kv_step_operands step{invocation->query, invocation->query_len, invocation->appended_key,
+                                  invocation->appended_key_len, invocation->appended_value,
+                                  invocation->appended_value_len};
+    pvlc_hip_status st = execute_step(s, &step, execution->attention, nullptr);
+    if (st == PVLC_HIP_OK) st = read_planes(s, execution->key_cache, execution->value_cache);
+    free_session_buffers(s);
+    delete s;
+    if (st != PVLC_HIP_OK) return st;
+    execution->cache_tokens = sp.cache_tokens_after;
+    execution->cache_capacity = plan.cache_capacity;
+    execution->queue_wall_time_ns = now_ns() - started;
+    return ok();
+}
+
+uint32_t pvlc_hip_paged_decode_partition(uint32_t num_seqs, uint32_t max_context) {
+    return auto_partition(num_seqs, max_context);
+}
+
+size_t pvlc_hip_paged_decode_workspace_bytes(uint32_t num_seqs, uint32_t max_context, uint32_t partition_tokens) {
+    if (num_seqs == 0 || max_context == 0) return 0;
+    const uint32_t p = partition_tokens ? partition_tokens : auto_partition(num_seqs, max_context);
+    if (p < 64 || p % 64 != 0) return 0;
+    return decode_workspace_layout(num_seqs, (max_context + p - 1) / p).total;
+}
+
+pvlc_hip_status pvlc_hip_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
+    if (!workspace || workspace_bytes % 4 != 0)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "workspace must be non-NULL and a multiple of 4 bytes");
+    const int e = launch_fill_u32(static_cast<uint32_t *>(workspace), workspace_bytes / 4, 0u, stream);
+    if (e != 0) return hip_fail(static_cast<hipError_t>(e), "workspace init");
+    return ok();
+}
+
+pvlc_hip_status pvlc_hip_workspace_error(const void *workspace, size_t workspace_bytes, void *stream,
+                                         uint32_t *error_out) {
+    if (!workspace || !error_out || workspace_bytes < 256)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "workspace too small");
+    // The error word is the first word of every decode workspace.
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    HIP_TRY(hipMemcpyAsync(error_out, workspace, sizeof(uint32_t), hipMemcpyDeviceToHost, st), "error word readback");
+    HIP_TRY(hipStreamSynchronize(st), "error word readback");
+    return ok();
+}
+
+pvlc_hip_status pvlc_hip_paged_decode_f16(const pvlc_hip_paged_decode_args *args, void *stream) {
+    if (pvlc_hip_status st = launch_decode_checked(args, stream)) return st;
+    return ok();
+}
+
+pvlc_hip_status pvlc_hip_kv_pack_f16(const uint16_t *key_rows, const uint16_t *value_rows, uint32_t tokens,
+                                     const int32_t *block_table, uint32_t num_blocks, uint16_t *key_cache,
+                                     uint16_t *value_cache, void *stream) {
+    if (!key_rows || !value_rows || !key_cache || !value_cache)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "NULL buffer");
+    if (tokens == 0 || num_blocks == 0) return invalid(PVLC_HIP_INV_ZERO_DIMENSION, "tokens and blocks must be nonzero");
+    if (!block_table && (tokens + kBlockTokens - 1) / kBlockTokens > num_blocks)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "tokens exceed the contiguous blocks");
+    const int e = launch_kv_pack(key_rows, value_rows, tokens, block_table, num_blocks, key_cache, value_cache,
+                                 nullptr, stream);
+    if (e != 0) return hip_fail(static_cast<hipError_t>(e), "kv pack launch");
+    return ok();
+}
+
+pvlc_hip_status pvlc_hip_kv_unpack_f16(const uint16_t *key_cache, const uint16_t *value_cache, uint32_t tokens,
+                                       const int32_t *block_table, uint32_t num_blocks, uint16_t *key_rows,
+                                       uint16_t *value_rows, void *stream) {
+    if (!key_rows || !value_rows || !key_cache || !value_cache)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "NULL buffer");
+    if (tokens == 0 || num_blocks == 0) return invalid(PVLC_HIP_INV_ZERO_DIMENSION, "tokens and blocks must be nonzero");
+    if (!block_table && (tokens + kBlockTokens - 1) / kBlockTokens > num_blocks)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "tokens exceed the contiguous blocks");
+    const int e = launch_kv_unpack(key_cache, value_cache, tokens, block_table, num_blocks, key_rows, value_rows,
+                                   stream);
+    if (e != 0) return hip_fail(static_cast<hipError_t>(e), "kv unpack launch");
+    return ok();
+}
+
+pvlc_hip_status pvlc_hip_paged_prefill_f16(const pvlc_hip_paged_prefill_args *args, void *stream) {
+    if (!args) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill args are NULL");
+    if (args->tokens == 0 || args->num_blocks == 0)
+        return invalid(PVLC_HIP_INV_ZERO_DIMENSION, "tokens and blocks must be nonzero");
+    if (!args->query || !args->key || !args->value || !args->out || !args->key_cache || !args->value_cache ||
+        !args->query_scratch)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill buffer pointer is NULL");
+    if ((args->rope_cos == nullptr) != (args->rope_sin == nullptr) || (args->rope_cos && args->rope_rows == 0))
+        return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION, "rotary tables must be given together with rows");
+    if (!args->positions && args->rope_cos && args->tokens > args->rope_rows)
+        return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION, "rotary table shorter than the prefill");
+    if (!args->block_table && (args->tokens + kBlockTokens - 1) / kBlockTokens > args->num_blocks)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "tokens exceed the contiguous blocks");
+    const int e = launch_prefill(args, stream);
+    if (e != 0) return hip_fail(static_cast<hipError_t>(e), "prefill launch");
+    return ok();
+}
+
+}  // extern "C"

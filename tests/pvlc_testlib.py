@@ -1,0 +1,94 @@
+"""Shared helpers of the GPU parity tests: seeded fp16 inputs, host packing
+into the blocked device layout (independent numpy code), and the tolerance
+check of the north star (fp16 output, f32 accumulation: max-abs 2e-3 and
+relative L2 1e-2)."""
+
+import sys
+
+import numpy as np
+
+import oracle as O
+from __graft_entry__ import load_package
+
+pvlc = load_package()
+
+ATOL = 2e-3
+REL_L2 = 1e-2
+W = 256  # one cache row, both kv heads
+
+
+def f16_bits(seed, n, scale=1.0):
+    return O.normal_f16(seed, n, scale)
+
+
+def widen(bits):
+    return O.f16_to_f32(bits)
+
+
+def check_close(actual, expected, label="", atol=ATOL, rel=REL_L2):
+    actual = np.asarray(actual, np.float32).ravel()
+    expected = np.asarray(expected, np.float32).ravel()
+    assert np.all(np.isfinite(actual)), f"{label}: non-finite output"
+    err = np.abs(actual - expected)
+    max_abs = float(err.max())
+    rel_l2 = float(np.linalg.norm(actual - expected) / max(np.linalg.norm(expected), 1e-30))
+    print(f"[parity] {label}: max_abs={max_abs:.3e} rel_l2={rel_l2:.3e}", flush=True)
+    assert max_abs <= atol, f"{label}: max abs {max_abs} > {atol}"
+    assert rel_l2 <= rel, f"{label}: rel L2 {rel_l2} > {rel}"
+    return max_abs, rel_l2
+
+
+def scatter_rows(plane_k, plane_v, k_rows, v_rows, tokens, table):
+    """Write rows 0..tokens-1 of one sequence into blocked planes through its block table."""
+    t = np.arange(tokens)
+    blk = np.asarray(table)[t // 16]
+    tt = t % 16
+    for h in range(2):
+        for d in range(128):
+            kidx = ((blk * 2 + h) * 16 + d // 8) * 128 + tt * 8 + d % 8
+            vidx = ((blk * 2 + h) * 128 + d) * 16 + tt
+            plane_k[kidx] = k_rows.reshape(tokens, 2, 128)[:, h, d]
+            plane_v[vidx] = v_rows.reshape(tokens, 2, 128)[:, h, d]
+
+
+def gather_rows(plane_k, plane_v, tokens, table):
+    t = np.arange(tokens)
+    blk = np.asarray(table)[t // 16]
+    tt = t % 16
+    k = np.zeros((tokens, 2, 128), np.uint16)
+    v = np.zeros((tokens, 2, 128), np.uint16)
+    for h in range(2):
+        for d in range(128):
+            k[:, h, d] = plane_k[((blk * 2 + h) * 16 + d // 8) * 128 + tt * 8 + d % 8]
+            v[:, h, d] = plane_v[((blk * 2 + h) * 128 + d) * 16 + tt]
+    return k.ravel(), v.ravel()
+
+
+def rope_k_f16(k_bits, pos, base=500000.0):
+    """Oracle rotary on one appended row [2][128] at `pos`, rounded to fp16."""
+    rot = O.rope_neox_f32(widen(k_bits), 2, 128, 128, [pos, pos], base)
+    return O.f32_to_f16(rot)
+
+
+def to_dev(bits):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).cuda()
+
+
+def to_dev_i32(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).cuda()
+
+
+def to_dev_f32(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
+
+
+def from_dev(t):
+    return t.cpu().numpy().view(np.uint16).ravel()
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()

@@ -1,0 +1,356 @@
+"""GPU parity of the decode hot path against the CPU oracle.
+
+Inputs are seeded N(0,1) drawn as fp16; the oracle runs on the same values
+widened exactly to f32 (decode_gqa_f32, cpu-ref lib.rs:858-927).  Bars:
+appended rows and cache gathers bit-exact; attention within max-abs 2e-3 and
+relative L2 1e-2.  Mirrors the reference's native contract tests
+(crates/pvlc-runtime-native/tests/decoder_cached_gqa_native_contract.rs,
+decoder_kv_session_native_contract.rs).
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from pvlc_testlib import (W, check_close, f16_bits, from_dev, gather_rows, log, pvlc, rope_k_f16, scatter_rows,
+                          to_dev, to_dev_f32, to_dev_i32, widen)
+
+pytestmark = pytest.mark.gpu
+POISON = np.array([0x7FC051A7], np.uint32).view(np.float32)[0]  # runtime-core lib.rs:184
+
+
+@pytest.fixture(scope="module")
+def runtime():
+    rt = pvlc.NativeRuntime(0)
+    yield rt
+    rt.close()
+
+
+def session_inputs(seed, prefix, capacity):
+    keys = widen(f16_bits(seed, capacity * W))
+    values = widen(f16_bits(seed + 1, capacity * W))
+    keys[prefix * W:] = POISON
+    values[prefix * W:] = POISON
+    return keys, values
+
+
+def step_inputs(seed):
+    return widen(f16_bits(seed, 2048)), widen(f16_bits(seed + 1, W)), widen(f16_bits(seed + 2, W))
+
+
+def bits32(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def test_session_single_step_config1_shape(runtime):
+    prefix, capacity = 1024, 1040
+    log(f"case: session step prefix={prefix} capacity={capacity}")
+    keys, values = session_inputs(10, prefix, capacity)
+    q, k, v = step_inputs(20)
+    s = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(prefix, capacity, keys, values))
+    ex = s.step(pvlc.DecoderKvSessionStep(q, k, v))
+    assert ex.cache_tokens == prefix + 1 and s.cache_tokens == prefix + 1
+    ka = np.concatenate([keys[:prefix * W], k])
+    va = np.concatenate([values[:prefix * W], v])
+    check_close(ex.attention, O.decode_gqa_f32(q, ka, va, prefix + 1, 16, 2, 128), "session T=1025")
+    snap = s.finish()
+    assert snap.cache_tokens == prefix + 1 and snap.cache_capacity == capacity
+    np.testing.assert_array_equal(bits32(snap.key_cache[:(prefix + 1) * W]), bits32(ka))
+    np.testing.assert_array_equal(bits32(snap.value_cache[:(prefix + 1) * W]), bits32(va))
+    assert np.all(np.isnan(snap.key_cache[(prefix + 1) * W:]))  # poison tail kept (as fp16 NaN)
+
+
+@pytest.mark.parametrize("prefix", [1, 2, 15, 16, 17, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 1023, 2047])
+def test_session_prefix_sweep(runtime, prefix):
+    capacity = prefix + 1 + (prefix % 7)
+    log(f"case: prefix sweep prefix={prefix} capacity={capacity}")
+    keys, values = session_inputs(1000 + prefix, prefix, capacity)
+    q, k, v = step_inputs(2000 + prefix)
+    s = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(prefix, capacity, keys, values))
+    out = s.step(pvlc.DecoderKvSessionStep(q, k, v)).attention
+    ka = np.concatenate([keys[:prefix * W], k])
+    va = np.concatenate([values[:prefix * W], v])
+    check_close(out, O.decode_gqa_f32(q, ka, va, prefix + 1, 16, 2, 128), f"prefix={prefix}")
+
+
+def test_session_persistent_steps_and_finish_snapshot(runtime):
+    prefix, capacity, steps = 300, 310, 5
+    log("case: persistent session 5 steps")
+    keys, values = session_inputs(30, prefix, capacity)
+    s = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(prefix, capacity, keys, values))
+    ka, va = keys[:prefix * W].copy(), values[:prefix * W].copy()
+    for i in range(steps):
+        q, k, v = step_inputs(40 + 3 * i)
+        out = s.step(pvlc.DecoderKvSessionStep(q, k, v)).attention
+        ka, va = np.concatenate([ka, k]), np.concatenate([va, v])
+        t = prefix + 1 + i
+        check_close(out, O.decode_gqa_f32(q, ka, va, t, 16, 2, 128), f"step {i} T={t}")
+    snap = s.finish()
+    assert snap.cache_tokens == prefix + steps
+    np.testing.assert_array_equal(bits32(snap.key_cache[:(prefix + steps) * W]), bits32(ka))
+    np.testing.assert_array_equal(bits32(snap.value_cache[:(prefix + steps) * W]), bits32(va))
+    with pytest.raises(pvlc.PvlcHipError):
+        s.step(pvlc.DecoderKvSessionStep(*step_inputs(99)))  # consumed by finish
+
+
+def test_session_invalid_step_has_no_effect_and_capacity_exhaustion(runtime):
+    prefix, capacity = 5, 7
+    log("case: invalid step / exhaustion")
+    keys, values = session_inputs(50, prefix, capacity)
+    s = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(prefix, capacity, keys, values))
+    q, k, v = step_inputs(60)
+    bad = q.copy()
+    bad[0] = np.nan
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        s.step(pvlc.DecoderKvSessionStep(bad, k, v))
+    assert e.value.invocation_code == "NonFiniteInput" and s.cache_tokens == prefix and not s.poisoned
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        s.step(pvlc.DecoderKvSessionStep(q, k[:-1], v))
+    assert e.value.invocation_code == "LengthMismatch" and s.cache_tokens == prefix
+    big = k.copy()
+    big[3] = 1e6  # finite f32 outside fp16 storage
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        s.step(pvlc.DecoderKvSessionStep(q, big, v))
+    assert e.value.invocation_code == "NonFiniteInput" and s.cache_tokens == prefix
+    s.step(pvlc.DecoderKvSessionStep(q, k, v))
+    s.step(pvlc.DecoderKvSessionStep(q, k, v))
+    assert s.cache_tokens == capacity
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        s.step(pvlc.DecoderKvSessionStep(q, k, v))
+    assert e.value.invocation_code == "InvalidDecoderGeometry" and s.cache_tokens == capacity
+    snap = s.finish()
+    np.testing.assert_array_equal(bits32(snap.key_cache[:prefix * W]), bits32(keys[:prefix * W]))
+
+
+def test_session_failure_after_submission_poisons(runtime):
+    log("case: injected failure poisons")
+    keys, values = session_inputs(70, 4, 8)
+    s = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(4, 8, keys, values))
+    s.fail_next_step_after_submit()
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        s.step(pvlc.DecoderKvSessionStep(*step_inputs(80)))
+    assert e.value.code == "Operation" and s.poisoned and s.cache_tokens == 4
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        s.step(pvlc.DecoderKvSessionStep(*step_inputs(81)))
+    assert e.value.code == "Operation"
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        s.finish()
+    assert e.value.code == "Operation"
+
+
+def test_interleaved_sessions_stay_independent(runtime):
+    log("case: interleaved sessions")
+    a_k, a_v = session_inputs(90, 33, 40)
+    b_k, b_v = session_inputs(91, 70, 80)
+    a = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(33, 40, a_k, a_v))
+    b = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(70, 80, b_k, b_v))
+    qa, ka, va = step_inputs(92)
+    qb, kb, vb = step_inputs(93)
+    oa = a.step(pvlc.DecoderKvSessionStep(qa, ka, va)).attention
+    ob = b.step(pvlc.DecoderKvSessionStep(qb, kb, vb)).attention
+    check_close(oa, O.decode_gqa_f32(qa, np.concatenate([a_k[:33 * W], ka]), np.concatenate([a_v[:33 * W], va]),
+                                     34, 16, 2, 128), "session a")
+    check_close(ob, O.decode_gqa_f32(qb, np.concatenate([b_k[:70 * W], kb]), np.concatenate([b_v[:70 * W], vb]),
+                                     71, 16, 2, 128), "session b")
+
+
+def test_cached_gqa_one_shot(runtime):
+    prefix, capacity = 200, 256
+    log("case: run_decoder_cached_gqa")
+    keys, values = session_inputs(100, prefix, capacity)
+    q, k, v = step_inputs(110)
+    ex = runtime.run_decoder_cached_gqa(pvlc.DecoderCachedGqaInvocation(prefix, capacity, q, k, v, keys, values))
+    assert ex.cache_tokens == prefix + 1 and ex.cache_capacity == capacity
+    ka = np.concatenate([keys[:prefix * W], k])
+    va = np.concatenate([values[:prefix * W], v])
+    check_close(ex.attention, O.decode_gqa_f32(q, ka, va, prefix + 1, 16, 2, 128), "cached gqa")
+    np.testing.assert_array_equal(bits32(ex.key_cache[:(prefix + 1) * W]), bits32(ka))
+    np.testing.assert_array_equal(bits32(ex.value_cache[:(prefix + 1) * W]), bits32(va))
+
+
+def test_wrong_grouping_would_be_detected(runtime):
+    # decoder_cached_gqa_native_contract.rs:248-272: the GPU result is far from a
+    # swapped-group oracle, so the tolerance check has teeth.
+    prefix, capacity = 64, 80
+    keys, values = session_inputs(120, prefix, capacity)
+    q, k, v = step_inputs(130)
+    out = runtime.run_decoder_cached_gqa(
+        pvlc.DecoderCachedGqaInvocation(prefix, capacity, q, k, v, keys, values)).attention
+    ka = np.concatenate([keys[:prefix * W], k])
+    va = np.concatenate([values[:prefix * W], v])
+    wrong = O.independent_decode_gqa_f32(q, ka, va, prefix + 1, 16, 2, 128, rotate_groups=True)
+    assert np.max(np.abs(out - wrong)) > 0.05
+
+
+def device_decode(layers, prefix, capacity, seed, rope=True, rotate_query=False, partition=0, positions=None):
+    """Contiguous per-layer caches (block_tables NULL), one launch for all layers."""
+    import torch
+    nb_per = (capacity + 15) // 16
+    kp = np.zeros(layers * nb_per * 16 * W, np.uint16)
+    vp = np.zeros_like(kp)
+    rows_k, rows_v = [], []
+    for l in range(layers):
+        rk, rv = f16_bits(seed + 10 * l, prefix * W), f16_bits(seed + 10 * l + 1, prefix * W)
+        table = np.arange(l * nb_per, (l + 1) * nb_per)
+        scatter_rows(kp, vp, rk, rv, prefix, table)
+        rows_k.append(rk)
+        rows_v.append(rv)
+    q = f16_bits(seed + 7, layers * 2048)
+    nk = f16_bits(seed + 8, layers * W)
+    nv = f16_bits(seed + 9, layers * W)
+    rows = max(capacity, 1) + 8
+    cos, sin = pvlc.rope_table(500000.0, rows)
+    d_k, d_v, d_q, d_nk, d_nv = to_dev(kp), to_dev(vp), to_dev(q), to_dev(nk), to_dev(nv)
+    d_out = torch.zeros(layers * 2048, dtype=torch.int16, device="cuda")
+    d_cos, d_sin = to_dev_f32(cos), to_dev_f32(sin)
+    d_pos = to_dev_i32(positions) if positions is not None else None
+    wsb = pvlc.decode_workspace_bytes(layers, capacity, partition)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    pvlc.workspace_init(ws, wsb)
+    args = pvlc.paged_decode_args(num_seqs=layers, num_blocks=layers * nb_per, max_blocks_per_seq=nb_per,
+                                  key_cache=d_k, value_cache=d_v, query=d_q, new_key=d_nk, new_value=d_nv,
+                                  out=d_out, workspace=ws, workspace_bytes=wsb, max_context=capacity,
+                                  uniform_cache_len=prefix, rope_cos=d_cos if rope else None,
+                                  rope_sin=d_sin if rope else None, rope_rows=rows if rope else 0,
+                                  positions=d_pos, rotate_query=rotate_query, partition_tokens=partition)
+    pvlc.paged_decode_f16(args)
+    torch.cuda.synchronize()
+    assert pvlc.workspace_error(ws, wsb) == 0
+    out = from_dev(d_out)
+    kp2, vp2 = from_dev(d_k), from_dev(d_v)
+    return dict(q=q, nk=nk, nv=nv, rows_k=rows_k, rows_v=rows_v, out=out, kp=kp2, vp=vp2, nb_per=nb_per,
+                cos=cos, sin=sin)
+
+
+def check_device_layers(r, layers, prefix, rope=True, rotate_query=False, positions=None, label=""):
+    for l in range(layers):
+        pos = prefix if positions is None else int(positions[l])
+        nk = r["nk"][l * W:(l + 1) * W]
+        nk_rot = rope_k_f16(nk, pos) if rope else nk
+        table = np.arange(l * r["nb_per"], (l + 1) * r["nb_per"])
+        gk, gv = gather_rows(r["kp"], r["vp"], prefix + 1, table)
+        # cache: prefix untouched, appended (rotated) row bit-exact
+        np.testing.assert_array_equal(gk, np.concatenate([r["rows_k"][l], nk_rot]))
+        np.testing.assert_array_equal(gv, np.concatenate([r["rows_v"][l], r["nv"][l * W:(l + 1) * W]]))
+        q = widen(r["q"][l * 2048:(l + 1) * 2048])
+        if rotate_query:
+            q = O.rope_neox_f32(q, 16, 128, 128, [pos] * 16, 500000.0)
+        want = O.decode_gqa_f32(q, widen(gk), widen(gv), prefix + 1, 16, 2, 128)
+        check_close(widen(r["out"][l * 2048:(l + 1) * 2048]), want, f"{label} layer {l}")
+
+
+def test_config1_rotary_append_at_1024():
+    log("case: config 1 (prefix 1024, rotary K at pos 1024, base 500000)")
+    r = device_decode(1, 1024, 1040, seed=500)
+    check_device_layers(r, 1, 1024, label="config1")
+
+
+@pytest.mark.parametrize("partition", [0, 64, 128, 256, 512, 1024])
+def test_config2_18_layers_at_2048(partition):
+    log(f"case: config 2 step (18 layers, T=2048, partition={partition})")
+    r = device_decode(18, 2047, 2304, seed=600, partition=partition)
+    check_device_layers(r, 18, 2047, label=f"config2 p={partition}")
+
+
+def test_rotated_query_and_explicit_positions():
+    log("case: rotate query, explicit positions")
+    positions = np.array([3, 900, 17], np.int32)
+    r = device_decode(3, 700, 720, seed=700, rotate_query=True, positions=positions)
+    check_device_layers(r, 3, 700, rotate_query=True, positions=positions, label="rotq")
+
+
+def test_no_rotary_small_contexts():
+    for prefix in (0, 1, 15, 16, 63, 64):
+        log(f"case: no rotary prefix={prefix}")
+        r = device_decode(2, prefix, max(prefix + 1, 16), seed=800 + prefix, rope=False)
+        check_device_layers(r, 2, prefix, rope=False, label=f"norope p={prefix}")
+
+
+def paged_case(num_seqs, lo, hi, seed, partition=0, log_uniform=False):
+    """Ragged batch over a shared paged cache with seeded permuted block tables."""
+    import torch
+    rng = np.random.default_rng(seed)
+    if log_uniform:
+        lens = np.exp(rng.uniform(np.log(lo), np.log(hi), num_seqs)).astype(np.int64)
+    else:
+        lens = rng.integers(lo, hi + 1, num_seqs)
+    cache_lens = lens - 1  # rows already cached; the step appends one
+    max_context = int(lens.max())
+    max_blocks = (max_context + 15) // 16
+    need = [(int(t) + 15) // 16 for t in lens]
+    num_blocks = sum(need) + 5
+    perm = rng.permutation(num_blocks)
+    tables = np.full((num_seqs, max_blocks), -1, np.int32)
+    kp = np.zeros(num_blocks * 16 * W, np.uint16)
+    vp = np.zeros_like(kp)
+    off = 0
+    rows = []
+    for s in range(num_seqs):
+        tables[s, :need[s]] = perm[off:off + need[s]]
+        off += need[s]
+        n = int(cache_lens[s])
+        rk, rv = f16_bits(seed * 100 + 2 * s, n * W), f16_bits(seed * 100 + 2 * s + 1, n * W)
+        if n:
+            scatter_rows(kp, vp, rk, rv, n, tables[s])
+        rows.append((rk, rv))
+    q = f16_bits(seed + 1, num_seqs * 2048)
+    nk = f16_bits(seed + 2, num_seqs * W)
+    nv = f16_bits(seed + 3, num_seqs * W)
+    cos, sin = pvlc.rope_table(500000.0, max_context + 1)
+    d_k, d_v = to_dev(kp), to_dev(vp)
+    d_out = torch.zeros(num_seqs * 2048, dtype=torch.int16, device="cuda")
+    wsb = pvlc.decode_workspace_bytes(num_seqs, max_context, partition)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    pvlc.workspace_init(ws, wsb)
+    keep = [to_dev(q), to_dev(nk), to_dev(nv), to_dev_i32(tables), to_dev_i32(cache_lens), to_dev_f32(cos),
+            to_dev_f32(sin)]
+    args = pvlc.paged_decode_args(num_seqs=num_seqs, num_blocks=num_blocks, max_blocks_per_seq=max_blocks,
+                                  key_cache=d_k, value_cache=d_v, query=keep[0], new_key=keep[1], new_value=keep[2],
+                                  out=d_out, workspace=ws, workspace_bytes=wsb, max_context=max_context,
+                                  block_tables=keep[3], cache_lens=keep[4], rope_cos=keep[5], rope_sin=keep[6],
+                                  rope_rows=max_context + 1, partition_tokens=partition)
+    pvlc.paged_decode_f16(args)
+    torch.cuda.synchronize()
+    assert pvlc.workspace_error(ws, wsb) == 0
+    out, kp2, vp2 = from_dev(d_out), from_dev(d_k), from_dev(d_v)
+    for s in range(num_seqs):
+        n = int(cache_lens[s])
+        gk, gv = gather_rows(kp2, vp2, n + 1, tables[s])
+        nk_rot = rope_k_f16(nk[s * W:(s + 1) * W], n)
+        np.testing.assert_array_equal(gk, np.concatenate([rows[s][0], nk_rot]))
+        np.testing.assert_array_equal(gv, np.concatenate([rows[s][1], nv[s * W:(s + 1) * W]]))
+        want = O.decode_gqa_f32(widen(q[s * 2048:(s + 1) * 2048]), widen(gk), widen(gv), n + 1, 16, 2, 128)
+        check_close(widen(out[s * 2048:(s + 1) * 2048]), want, f"paged seq {s} T={n + 1}")
+
+
+@pytest.mark.parametrize("partition", [0, 64, 512])
+def test_paged_ragged_batch(partition):
+    log(f"case: paged ragged 12 seqs partition={partition}")
+    paged_case(12, 1, 3000, seed=900 + partition, partition=partition)
+
+
+def test_paged_long_context_split_k():
+    log("case: paged long context (8 seqs, log-uniform [1024, 9000], partition 512)")
+    paged_case(8, 1024, 9000, seed=950, partition=512, log_uniform=True)
+
+
+def test_pack_unpack_roundtrip_through_block_table():
+    import torch
+    log("case: pack/unpack")
+    tokens, num_blocks = 100, 12
+    rng = np.random.default_rng(5)
+    table = rng.permutation(num_blocks)[:7].astype(np.int32)
+    k, v = f16_bits(1, tokens * W), f16_bits(2, tokens * W)
+    d_k = torch.zeros(num_blocks * 16 * W, dtype=torch.int16, device="cuda")
+    d_v = torch.zeros_like(d_k)
+    d_t = to_dev_i32(table)
+    pvlc.kv_pack_f16(to_dev(k), to_dev(v), tokens, d_k, d_v, num_blocks, block_table=d_t)
+    kp, vp = np.zeros(num_blocks * 16 * W, np.uint16), np.zeros(num_blocks * 16 * W, np.uint16)
+    scatter_rows(kp, vp, k, v, tokens, table)
+    np.testing.assert_array_equal(from_dev(d_k), kp)
+    np.testing.assert_array_equal(from_dev(d_v), vp)
+    ok, ov = torch.zeros(tokens * W, dtype=torch.int16, device="cuda"), torch.zeros(tokens * W, dtype=torch.int16,
+                                                                                      device="cuda")
+    pvlc.kv_unpack_f16(d_k, d_v, tokens, ok, ov, num_blocks, block_table=d_t)
+    np.testing.assert_array_equal(from_dev(ok), k)
+    np.testing.assert_array_equal(from_dev(ov), v)
