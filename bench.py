@@ -1,0 +1,254 @@
+"""Decode-attention benchmark: 18-layer GQA decode step at 2k context on one MI355X.
+
+Workload (measured at T = 2048): 18 decoder layers,
+each with its own fp16 KV cache (2 kv heads, head_dim 128, capacity 2304);
+one step appends one token per layer at row 2047 (K rotated, base 500000)
+and runs GQA attention (16 query heads) over the 2048 rows, for all layers in
+one launch of the fused paged-decode kernel.
+
+HBM, not cache: one 18-layer cache is ~41 MB and would sit in the 256 MB
+Infinity Cache if re-read back to back, so the timed steps rotate through
+enough independent replicas (> 256 MB together) that every step streams its
+keys and values from HBM.  The single-replica (cache-warm) figure is reported
+separately as ``warm_single_replica``.
+
+Timing: HIP events on the stream the kernel is launched on, around K
+back-to-back steps (the host queues them behind a GPU-side delay so launch
+latency on the host does not leave the GPU idle).
+
+CPU baseline: the oracle's C restatement of pvlc-cpu-ref (rope_neox +
+append_decoder_kv_cache + decode_gqa_f32, single thread) on the same replica-0
+inputs, over a bounded sample of whole steps.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+LAYERS = 18
+CONTEXT = 2048  # rows attended after the append
+CAPACITY = 2304  # 1280 + 1024 (config 2's last context)
+ROPE_BASE = 500000.0
+HBM_PEAK_GBPS = 8000.0
+W = 256
+
+
+def algorithmic_bytes(t: int) -> int:
+    """K,V reads (1024*T) + q (4096) + out (4096) + new K/V read (1024) + append write (1024), per layer."""
+    return 1024 * t + 10240
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = automatic)")
+    ap.add_argument("--replicas", type=int, default=12)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-steps", type=int, default=0,
+                    help="only run this many steps (no CPU leg), for rocprofv3 runs")
+    return ap.parse_args()
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from __graft_entry__ import load_package
+
+    pvlc = load_package()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    nb_per = CAPACITY // 16
+    plane = LAYERS * nb_per * 16 * W  # fp16 elements per plane per replica
+    prefix = CONTEXT - 1
+
+    # Replica 0 comes from host arrays (so the CPU baseline sees the same
+    # values); the others are drawn on the device.
+    rng = np.random.default_rng(2048)
+    host_k = rng.standard_normal((LAYERS, CAPACITY * W), dtype=np.float32).astype(np.float16)
+    host_v = rng.standard_normal((LAYERS, CAPACITY * W), dtype=np.float32).astype(np.float16)
+    host_q = rng.standard_normal((LAYERS, 2048), dtype=np.float32).astype(np.float16)
+    host_nk = rng.standard_normal((LAYERS, W), dtype=np.float32).astype(np.float16)
+    host_nv = rng.standard_normal((LAYERS, W), dtype=np.float32).astype(np.float16)
+    gen = torch.Generator(device=dev).manual_seed(7)
+
+    cos, sin = pvlc.rope_table(ROPE_BASE, CAPACITY)
+    d_cos = torch.from_numpy(cos.ravel()).to(dev)
+    d_sin = torch.from_numpy(sin.ravel()).to(dev)
+    wsb = pvlc.decode_workspace_bytes(LAYERS, CAPACITY, args.partition)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    pvlc.workspace_init(ws, wsb, stream)
+
+    replicas = []
+    for r in range(args.replicas):
+        if r == 0:
+            kp = torch.empty(plane, dtype=torch.float16, device=dev)
+            vp = torch.empty(plane, dtype=torch.float16, device=dev)
+            rows_k = torch.from_numpy(host_k).to(dev)
+            rows_v = torch.from_numpy(host_v).to(dev)
+            for l in range(LAYERS):
+                off = l * nb_per * 16 * W
+                pvlc.kv_pack_f16(rows_k[l], rows_v[l], CAPACITY, kp[off:], vp[off:], nb_per, stream=stream)
+            q = torch.from_numpy(host_q).to(dev)
+            nk = torch.from_numpy(host_nk).to(dev)
+            nv = torch.from_numpy(host_nv).to(dev)
+            del rows_k, rows_v
+        else:
+            kp = torch.randn(plane, generator=gen, device=dev, dtype=torch.float32).half()
+            vp = torch.randn(plane, generator=gen, device=dev, dtype=torch.float32).half()
+            q = torch.randn(LAYERS * 2048, generator=gen, device=dev, dtype=torch.float32).half()
+            nk = torch.randn(LAYERS * W, generator=gen, device=dev, dtype=torch.float32).half()
+            nv = torch.randn(LAYERS * W, generator=gen, device=dev, dtype=torch.float32).half()
+        out = torch.empty(LAYERS * 2048, dtype=torch.float16, device=dev)
+        a = pvlc.paged_decode_args(num_seqs=LAYERS, num_blocks=LAYERS * nb_per, max_blocks_per_seq=nb_per,
+                                   key_cache=kp, value_cache=vp, query=q, new_key=nk, new_value=nv, out=out,
+                                   workspace=ws, workspace_bytes=wsb, max_context=CAPACITY,
+                                   uniform_cache_len=prefix, rope_cos=d_cos, rope_sin=d_sin, rope_rows=CAPACITY,
+                                   partition_tokens=args.partition)
+        replicas.append(dict(args=a, keep=(kp, vp, q, nk, nv, out)))
+    torch.cuda.synchronize()
+    replica_bytes = 2 * plane * 2
+    partition = args.partition or pvlc.decode_partition(LAYERS, CAPACITY)
+
+    def run(n, rot):
+        for i in range(n):
+            pvlc.paged_decode_f16(replicas[i % rot]["args"], stream)
+
+    if args.profile_steps:
+        run(args.profile_steps, len(replicas))
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_steps": args.profile_steps, "partition": partition}))
+        return 0
+
+    def timed(k, rot):
+        torch.cuda.synchronize()
+        # Keep the GPU busy while the host queues k launches, then time only them.
+        torch.cuda._sleep(int(2_000_000 + 40_000 * k))
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        run(k, rot)
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / k  # ms per step
+
+    run(args.warmup, len(replicas))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms_per_step = timed(args.steps, len(replicas))
+    wall = time.perf_counter() - t0
+    warm_ms = timed(args.steps, 1)
+    err = pvlc.workspace_error(ws, wsb, stream)
+
+    step_bytes = LAYERS * algorithmic_bytes(CONTEXT)
+    us = ms_per_step * 1e3
+    gbps = step_bytes / (ms_per_step * 1e-3) / 1e9
+    warm_gbps = step_bytes / (warm_ms * 1e-3) / 1e9
+
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", "decode18_t2048_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": "decode-attn µs/step + achieved HBM GB/s (% peak), 18 layers, 2k ctx, 1 GPU",
+        "value": round(us, 3),
+        "unit": "µs/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 (f32 accumulate)",
+        "data": "synthetic N(0,1) fp16, seeded",
+        "config": {"workload": "config 2 decode step at T=2048: 18 layers x (rotary K append + GQA 16q/2kv "
+                               "d128 over 2048 rows), one fused launch",
+                   "layers": LAYERS, "context": CONTEXT, "cache_capacity": CAPACITY,
+                   "partition_tokens": partition, "replicas_rotated": len(replicas),
+                   "replica_bytes": replica_bytes},
+        "achieved_gbps": round(gbps, 1),
+        "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "warm_single_replica": {"us_per_step": round(warm_ms * 1e3, 3), "gbps": round(warm_gbps, 1),
+                                "note": "one replica re-read back to back: served largely from the Infinity "
+                                        "Cache, not HBM"},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": step_bytes},
+        "device_error_word": err,
+        "timed_wall_s": round(wall, 3),
+    }
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(host_q, host_k, host_v, host_nk, host_nv, cos, sin, args.cpu_seconds,
+                                              step_bytes, replicas[0]["keep"][5])
+    print(json.dumps(result, ensure_ascii=False))
+    return 0
+
+
+def cpu_baseline(host_q, host_k, host_v, host_nk, host_nv, cos, sin, seconds, step_bytes, gpu_out):
+    """pvlc-cpu-ref restated in C (oracle/), single thread: per layer rope_neox on
+    the new key, append_decoder_kv_cache (prefix copy + row), decode_gqa_f32."""
+    import oracle as O
+
+    prefix = CONTEXT - 1
+    qf = host_q.astype(np.float32)
+    kf = host_k[:, :prefix * W].astype(np.float32)
+    vf = host_v[:, :prefix * W].astype(np.float32)
+    nkf = host_nk.astype(np.float32)
+    nvf = host_nv.astype(np.float32)
+    outs = None
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        outs = []
+        for l in range(LAYERS):
+            rot = O.rope_neox_f32(nkf[l], 2, 128, 128, [prefix, prefix], ROPE_BASE)
+            rot = O.f16_to_f32(O.f32_to_f16(rot))  # stored as fp16, like the device cache
+            keys, values = O.append_kv_f32(kf[l], vf[l], prefix, rot, nvf[l], 2, 128)
+            outs.append(O.decode_gqa_f32(qf[l], keys, values, CONTEXT, 16, 2, 128))
+        steps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds or steps >= 200:
+            break
+    per_step = elapsed / steps
+    gpu = gpu_out.float().cpu().numpy().reshape(LAYERS, 2048)
+    max_err = float(np.max(np.abs(gpu - np.stack(outs))))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(per_step * 1e6, 1), "unit": "µs/step", "cores": 1, "kind": "port",
+            "gbps": round(step_bytes / per_step / 1e9, 3),
+            "sample": f"{steps} full 18-layer steps at T=2048 on replica 0 ({elapsed:.1f} s)",
+            "host": {"nproc": os.cpu_count(), "cpu": model},
+            "gpu_vs_cpu_max_abs": max_err}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -26,7 +26,8 @@ from dataclasses import dataclass
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIBRARY_PATH = os.path.join(_HERE, "libpvlc_hip.so")
+# PVLC_HIP_LIBRARY selects another build of the same C ABI (default: in-tree).
+LIBRARY_PATH = os.environ.get("PVLC_HIP_LIBRARY", os.path.join(_HERE, "libpvlc_hip.so"))
 
 QUERY_HEADS = 16
 KV_HEADS = 2
@@ -188,6 +189,14 @@ def _load() -> ctypes.CDLL:
     if not os.path.exists(LIBRARY_PATH):
         raise ImportError(f"{LIBRARY_PATH} is missing: build it with __graft_entry__.build() "
                           "(there is no CPU fallback for this backend)")
+    # One HIP runtime per process: PyTorch bundles its own libamdhip64.so.7.
+    # Loading it first lets this library's libamdhip64.so.7 dependency bind to
+    # that copy (same SONAME) instead of mapping a second runtime, which would
+    # leave one of the two without devices.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(LIBRARY_PATH)
     for name, (argtypes, restype) in SIGNATURES.items():
         fn = getattr(lib, name)

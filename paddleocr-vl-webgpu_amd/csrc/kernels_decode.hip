@@ -14,6 +14,11 @@
 // Softmax statistics use cross-lane shuffles; waves combine through LDS; the
 // last partition to finish (device-scope counter) merges all partitions.
 //
+// Latency discipline (the whole step is a few microseconds): every wave
+// issues its first chunk's loads before anything else; block ids come from
+// scalar loads; the appended row is rotated with vector loads while those
+// loads are in flight; the merge loads partials in batches.
+//
 // Reference behaviour replaced: decoder_kv_append_f32, decoder_mrope_f32 (k
 // and optionally q), decoder_gqa_split_partial_f32 and
 // decoder_gqa_split_merge_f32 (crates/pvlc-wgsl/src/lib.rs:927-952,
@@ -32,9 +37,11 @@ namespace {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kChunkTokens = 64;  // tokens a wave holds in registers at once
 constexpr int kTilesPerChunk = kChunkTokens / 16;
+constexpr int kMaxParts = static_cast<int>(kMaxMergeParts);
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeParams {
@@ -63,35 +70,46 @@ struct DecodeParams {
     float scale_log2;   // log2(e)/sqrt(128)
 };
 
-__device__ inline float to_f32(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 __device__ inline _Float16 to_h(float f) { return static_cast<_Float16>(f); }
 
-// Rotate-half of 8 consecutive dims [d0, d0+8) of one head row (fp16 in HBM),
+// Read a wave-uniform element of a buffer the kernel never writes (block
+// tables, cache lengths, positions) through the constant address space, so
+// it becomes a scalar load that does not wait behind the vector loads.
+__device__ inline int32_t load_const(const int32_t *base, size_t index) {
+    typedef const __attribute__((address_space(4))) int32_t *constant_ptr;
+    return ((constant_ptr)base)[index];
+}
+
+// Rotate-half of 8 consecutive dims [d0, d0+8) of one head row:
 // x'[d] = x[d]*cos + partner*sin with partner = -x[d+64] (d < 64) or x[d-64],
 // exactly the f32 expression of apply_rope_neox / apply_multimodal_rope_f32
 // (cpu-ref lib.rs:459-463, :645-654); each product and the sum are rounded
 // separately (this file is compiled without FP contraction), then RNE to fp16.
 __device__ inline half8_t rotate_chunk(const uint16_t *row, int d0, const float *cos_row, const float *sin_row) {
-    const int partner0 = d0 < 64 ? d0 + 64 : d0 - 64;
-    const int i0 = d0 & 63;
+    const half8_t x = *reinterpret_cast<const half8_t *>(row + d0);
+    const half8_t y = *reinterpret_cast<const half8_t *>(row + (d0 < 64 ? d0 + 64 : d0 - 64));
+    const float4_t c0 = *reinterpret_cast<const float4_t *>(cos_row + (d0 & 63));
+    const float4_t c1 = *reinterpret_cast<const float4_t *>(cos_row + (d0 & 63) + 4);
+    const float4_t s0 = *reinterpret_cast<const float4_t *>(sin_row + (d0 & 63));
+    const float4_t s1 = *reinterpret_cast<const float4_t *>(sin_row + (d0 & 63) + 4);
+    const float sign = d0 < 64 ? -1.0f : 1.0f;
     half8_t r;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const float x = to_f32(row[d0 + j]);
-        const float y = to_f32(row[partner0 + j]);
-        const float partner = d0 < 64 ? -y : y;
-        const float c = cos_row[i0 + j];
-        const float s = sin_row[i0 + j];
-        const float xc = x * c;
-        const float ps = partner * s;
+        const float c = j < 4 ? c0[j] : c1[j - 4];
+        const float s = j < 4 ? s0[j] : s1[j - 4];
+        const float xc = static_cast<float>(x[j]) * c;
+        const float ps = (sign * static_cast<float>(y[j])) * s;
         r[j] = to_h(xc + ps);
     }
     return r;
 }
 
+// Physical block of (sequence, tile); `tile` is wave-uniform so the table
+// read is a scalar load.
 __device__ inline uint32_t block_id(const DecodeParams &p, uint32_t seq, uint32_t tile) {
     if (p.block_tables == nullptr) return seq * p.max_blocks_per_seq + tile;
-    const int32_t b = p.block_tables[static_cast<size_t>(seq) * p.max_blocks_per_seq + tile];
+    const int32_t b = load_const(p.block_tables, static_cast<size_t>(seq) * p.max_blocks_per_seq + tile);
     if (b < 0 || static_cast<uint32_t>(b) >= p.num_blocks) {
         atomicOr(p.error_word, 2u);
         return 0;  // clamp: never address outside the planes
@@ -99,17 +117,42 @@ __device__ inline uint32_t block_id(const DecodeParams &p, uint32_t seq, uint32_
     return static_cast<uint32_t>(b);
 }
 
+// Issue the loads of one 64-token chunk starting at token ws.  Tiles at or
+// past part_end re-read the last valid tile (never outside the planes) and
+// are masked by the caller; loading unconditionally keeps the loads of all
+// four tiles back to back.
+__device__ inline void load_chunk(const DecodeParams &p, uint32_t s, uint32_t g, int ws, int part_end, int row,
+                                  int kg, half8_t (&kr)[kTilesPerChunk][4], half4_t (&vr)[kTilesPerChunk][8]) {
+    const int last_tile = (part_end - 1) >> 4;
+    uint32_t blk[kTilesPerChunk];
+#pragma unroll
+    for (int i = 0; i < kTilesPerChunk; ++i) blk[i] = block_id(p, s, static_cast<uint32_t>(min((ws >> 4) + i, last_tile)));
+#pragma unroll
+    for (int i = 0; i < kTilesPerChunk; ++i) {
+        const size_t slab = (static_cast<size_t>(blk[i]) * kKvHeads + g) * kBlockHeadElems;
+        const uint16_t *kbase = p.key_cache + slab;
+        const uint16_t *vbase = p.value_cache + slab;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+            kr[i][kb] = *reinterpret_cast<const half8_t *>(kbase + (kb * 4 + kg) * 128 + row * 8);
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            vr[i][c] = *reinterpret_cast<const half4_t *>(vbase + (c * 16 + row) * 16 + kg * 4);
+    }
+}
+
 template <int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void paged_decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParams p) {
     const uint32_t part = blockIdx.x;
     const uint32_t g = blockIdx.y;  // kv head
     const uint32_t s = blockIdx.z;  // sequence (or layer)
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int row = lane & 15;  // MFMA row/column index of this lane
     const int kg = lane >> 4;   // MFMA k-group of this lane
+    constexpr int kThreads = WAVES * 64;
 
-    const int64_t len_raw = p.cache_lens ? p.cache_lens[s] : static_cast<int64_t>(p.uniform_cache_len);
+    const int64_t len_raw = p.cache_lens ? load_const(p.cache_lens, s) : static_cast<int64_t>(p.uniform_cache_len);
     const int64_t capacity = static_cast<int64_t>(p.max_blocks_per_seq) * 16;
     const int64_t span = static_cast<int64_t>(p.max_parts) * p.partition_tokens;
     if (len_raw < 0 || len_raw + 1 > capacity || len_raw + 1 > span) {
@@ -124,9 +167,15 @@ __global__ __launch_bounds__(WAVES * 64) void paged_decode_kernel(DecodeParams p
     const int part_end = min(part_start + P, T);
     const int num_parts = (T + P - 1) / P;
 
+    // First chunk's keys and values: issued before anything else.
+    half8_t kr[kTilesPerChunk][4];
+    half4_t vr[kTilesPerChunk][8];
+    int ws = part_start + wave * kChunkTokens;
+    load_chunk(p, s, g, ws, part_end, row, kg, kr, vr);
+
     // Rotary position of the appended row (and of the query).
     bool rope = p.rope_cos != nullptr;
-    int pos = p.positions ? p.positions[s] : cache_len;
+    const int pos = p.positions ? load_const(p.positions, s) : cache_len;
     if (rope && (pos < 0 || static_cast<uint32_t>(pos) >= p.rope_rows)) {
         if (threadIdx.x == 0) atomicOr(p.error_word, 4u);
         rope = false;
@@ -143,21 +192,46 @@ __global__ __launch_bounds__(WAVES * 64) void paged_decode_kernel(DecodeParams p
         for (int kb = 0; kb < 4; ++kb) {
             const int d0 = kb * 32 + kg * 8;
             if (row < static_cast<int>(kGroup)) {
-                if (rope && p.rotate_query) {
-                    qb[kb] = rotate_chunk(qrow, d0, cos_row, sin_row);
-                } else {
-                    qb[kb] = *reinterpret_cast<const half8_t *>(qrow + d0);
-                }
+                qb[kb] = (rope && p.rotate_query) ? rotate_chunk(qrow, d0, cos_row, sin_row)
+                                                  : *reinterpret_cast<const half8_t *>(qrow + d0);
             } else {
                 qb[kb] = half8_t{};
             }
         }
     }
 
+    // The workgroup whose partition holds the appended row rotates the new
+    // key once, writes the new K/V row into the cache, and keeps it in LDS to
+    // stand in for that row of its tile loads (which may see the old row).
     const int append_tile = cache_len >> 4;
     const int append_row = cache_len & 15;
-    const uint16_t *new_k = p.new_key + (static_cast<size_t>(s) * kKvHeads + g) * kHeadDim;
-    const uint16_t *new_v = p.new_value + (static_cast<size_t>(s) * kKvHeads + g) * kHeadDim;
+    __shared__ uint16_t sm_new_k[kHeadDim];
+    __shared__ uint16_t sm_new_v[kHeadDim];
+    const bool owns_append = (append_tile << 4) >= part_start && (append_tile << 4) < part_end;
+    if (owns_append) {
+        if (threadIdx.x < 32) {
+            const uint32_t blk = block_id(p, s, static_cast<uint32_t>(append_tile));
+            const size_t slab = (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems;
+            if (threadIdx.x < 16) {
+                const uint16_t *new_k = p.new_key + (static_cast<size_t>(s) * kKvHeads + g) * kHeadDim;
+                const int d0 = threadIdx.x * 8;
+                const half8_t nk = rope ? rotate_chunk(new_k, d0, cos_row, sin_row)
+                                        : *reinterpret_cast<const half8_t *>(new_k + d0);
+                *reinterpret_cast<half8_t *>(sm_new_k + d0) = nk;
+                *reinterpret_cast<half8_t *>(p.key_cache + slab + threadIdx.x * 128 + append_row * 8) = nk;
+            } else {
+                const uint16_t *new_v = p.new_value + (static_cast<size_t>(s) * kKvHeads + g) * kHeadDim;
+                const int d0 = (threadIdx.x - 16) * 8;
+                // A uint16 vector: scattering elements of a _Float16 vector
+                // with 16-bit stores stored element 0 eight times on gfx950.
+                const u16x8_t nv = *reinterpret_cast<const u16x8_t *>(new_v + d0);
+                *reinterpret_cast<u16x8_t *>(sm_new_v + d0) = nv;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) p.value_cache[slab + (d0 + j) * 16 + append_row] = nv[j];
+            }
+        }
+        __syncthreads();  // uniform: owns_append depends on the workgroup only
+    }
 
     float m_run = -INFINITY;  // running max (log2 units) of head `row`
     float l_run = 0.0f;       // this lane's share of the running sum
@@ -165,67 +239,45 @@ __global__ __launch_bounds__(WAVES * 64) void paged_decode_kernel(DecodeParams p
 #pragma unroll
     for (int c = 0; c < 8; ++c) o[c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int chunk = 0;; ++chunk) {
-        const int ws = part_start + (chunk * WAVES + wave) * kChunkTokens;
-        if (ws >= part_end) break;
+    for (int chunk = 0; ws < part_end; ++chunk, ws += WAVES * kChunkTokens) {
+        if (chunk > 0) load_chunk(p, s, g, ws, part_end, row, kg, kr, vr);
 
-        half8_t kr[kTilesPerChunk][4];
-        half4_t vr[kTilesPerChunk][8];
+        // Zero the values of tiles past the partition (their scores are
+        // masked to -inf, but a re-read tile may hold poison rows, and
+        // NaN * 0 would reach P.V).
 #pragma unroll
         for (int i = 0; i < kTilesPerChunk; ++i) {
-            const int ts = ws + i * 16;
-            if (ts < part_end) {
-                const uint32_t blk = block_id(p, s, static_cast<uint32_t>(ts >> 4));
-                const size_t slab = (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems;
-                const uint16_t *kbase = p.key_cache + slab;
-                const uint16_t *vbase = p.value_cache + slab;
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-                    kr[i][kb] = *reinterpret_cast<const half8_t *>(kbase + (kb * 4 + kg) * 128 + row * 8);
-#pragma unroll
-                for (int c = 0; c < 8; ++c)
-                    vr[i][c] = *reinterpret_cast<const half4_t *>(vbase + (c * 16 + row) * 16 + kg * 4);
-
-                if ((ts >> 4) == append_tile) {
-                    // The appended row: rotated key and value come from the
-                    // step operands, are written to the cache once, and stand
-                    // in for whatever the load returned for that row.
-                    if (row == append_row) {
-#pragma unroll
-                        for (int kb = 0; kb < 4; ++kb) {
-                            const int d0 = (kb * 4 + kg) * 8;
-                            half8_t nk = rope ? rotate_chunk(new_k, d0, cos_row, sin_row)
-                                              : *reinterpret_cast<const half8_t *>(new_k + d0);
-                            kr[i][kb] = nk;
-                            *reinterpret_cast<half8_t *>(p.key_cache + slab + (kb * 4 + kg) * 128 + row * 8) = nk;
-                        }
-                    }
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int r = kg * 4 + j;
-                        if (r == append_row) {
-#pragma unroll
-                            for (int c = 0; c < 8; ++c) {
-                                const uint16_t v = new_v[c * 16 + row];
-                                vr[i][c][j] = __builtin_bit_cast(_Float16, v);
-                                p.value_cache[slab + (c * 16 + row) * 16 + r] = v;
-                            }
-                        } else if (r > append_row) {
-                            // rows past the end may hold poison: keep NaN out of P.V
-#pragma unroll
-                            for (int c = 0; c < 8; ++c) vr[i][c][j] = static_cast<_Float16>(0.0f);
-                        }
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb) kr[i][kb] = half8_t{};
+            if (ws + i * 16 >= part_end) {
 #pragma unroll
                 for (int c = 0; c < 8; ++c) vr[i][c] = half4_t{};
             }
         }
+        // Patch the appended row; zero rows past it (they may hold poison).
+        const int ti = append_tile - (ws >> 4);
+        if (ti >= 0 && ti < kTilesPerChunk) {
+#pragma unroll
+            for (int i = 0; i < kTilesPerChunk; ++i) {
+                if (i != ti) continue;
+                if (row == append_row) {
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+                        kr[i][kb] = *reinterpret_cast<const half8_t *>(sm_new_k + (kb * 4 + kg) * 8);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = kg * 4 + j;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        if (r == append_row)
+                            vr[i][c][j] = __builtin_bit_cast(_Float16, sm_new_v[c * 16 + row]);
+                        else if (r > append_row)
+                            vr[i][c][j] = static_cast<_Float16>(0.0f);
+                    }
+                }
+            }
+        }
 
-        // Scores: lane holds tokens ts + kg*4 + r (r = 0..3) of head `row`.
+        // Scores: lane holds tokens ws + i*16 + kg*4 + r (r = 0..3) of head `row`.
         float x[kTilesPerChunk][4];
         float cmax = -INFINITY;
 #pragma unroll
@@ -291,7 +343,6 @@ __global__ __launch_bounds__(WAVES * 64) void paged_decode_kernel(DecodeParams p
     }
     __syncthreads();
 
-    constexpr int kThreads = WAVES * 64;
     constexpr int kPerThread = (kGroup * kHeadDim) / kThreads;
     float po[kPerThread], pm[kPerThread], pl[kPerThread];
 #pragma unroll
@@ -323,46 +374,89 @@ __global__ __launch_bounds__(WAVES * 64) void paged_decode_kernel(DecodeParams p
         return;
     }
 
+    // Cross-workgroup hand-off without L2 maintenance: partials, the arrival
+    // counter and the merge reads are relaxed agent-scope atomics (sc1), which
+    // are coherent across the XCDs' L2s by themselves.  Every store of the
+    // workgroup completes (s_waitcnt vmcnt(0), then the barrier) before thread
+    // 0 counts the arrival, which orders the partials before the count.
+    // (A C++ release/acquire fence at agent scope would instead write back and
+    // invalidate the whole L2 of the XCD in every workgroup.)
     const size_t unit = (static_cast<size_t>(s) * kKvHeads + g) * p.max_parts;
     float *part_o = p.part_o + (unit + part) * (kGroup * kHeadDim);
     float *part_ml = p.part_ml + (unit + part) * (2 * kGroup);
 #pragma unroll
     for (int e = 0; e < kPerThread; ++e) {
         const int idx = threadIdx.x + e * kThreads;
-        part_o[idx] = po[e];
+        __hip_atomic_store(part_o + idx, po[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if ((idx & 127) == 0) {
-            part_ml[idx >> 7] = pm[e];
-            part_ml[kGroup + (idx >> 7)] = pl[e];
+            __hip_atomic_store(part_ml + (idx >> 7), pm[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(part_ml + kGroup + (idx >> 7), pl[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    // Publish the partial, count arrivals; the last arrival merges.
-    __threadfence();
+    // Wait for this wave's partial stores to complete (a single-wave
+    // workgroup's __syncthreads() emits no wait), then for every wave.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(p.counters + s * kKvHeads + g, 1u);
+        const uint32_t prev = __hip_atomic_fetch_add(p.counters + s * kKvHeads + g, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
         sm_last = (prev == static_cast<uint32_t>(num_parts - 1));
     }
     __syncthreads();
     if (!sm_last) return;
-    __threadfence();
 
+    // Merge: stage every partition's (max, sum) in LDS, turn them into one
+    // weight per (partition, head), then sum the partial outputs with the
+    // loads of each batch of partitions in flight together.
     const float *all_o = p.part_o + unit * (kGroup * kHeadDim);
     const float *all_ml = p.part_ml + unit * (2 * kGroup);
+    __shared__ float sm_ml[kMaxParts * 2 * kGroup];
+    __shared__ float sm_w[kMaxParts * kGroup];
+    auto ld = [](const float *q) { return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    for (int i = threadIdx.x; i < num_parts * 2 * static_cast<int>(kGroup); i += kThreads) sm_ml[i] = ld(all_ml + i);
+    __syncthreads();
+    if (threadIdx.x < static_cast<int>(kGroup)) {
+        const int h = threadIdx.x;
+        float M = -INFINITY;
+        for (int q = 0; q < num_parts; ++q) M = fmaxf(M, sm_ml[q * 2 * kGroup + h]);
+        float L = 0.f;
+        for (int q = 0; q < num_parts; ++q) {
+            const float f = __builtin_amdgcn_exp2f(sm_ml[q * 2 * kGroup + h] - M);
+            sm_w[q * kGroup + h] = f;
+            L += sm_ml[q * 2 * kGroup + kGroup + h] * f;
+        }
+        const float inv = 1.0f / L;
+        for (int q = 0; q < num_parts; ++q) sm_w[q * kGroup + h] *= inv;
+    }
+    __syncthreads();
+    float acc[kPerThread];
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) acc[e] = 0.f;
+    constexpr int kBatch = 8;
+    for (int q0 = 0; q0 < num_parts; q0 += kBatch) {
+        float v[kBatch][kPerThread];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+            for (int e = 0; e < kPerThread; ++e)
+                v[b][e] = (q0 + b < num_parts)
+                              ? ld(all_o + static_cast<size_t>(q0 + b) * (kGroup * kHeadDim) + threadIdx.x + e * kThreads)
+                              : 0.f;
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+            for (int e = 0; e < kPerThread; ++e) {
+                const int h = (threadIdx.x + e * kThreads) >> 7;
+                acc[e] += (q0 + b < num_parts) ? v[b][e] * sm_w[(q0 + b) * kGroup + h] : 0.f;
+            }
+    }
 #pragma unroll
     for (int e = 0; e < kPerThread; ++e) {
         const int idx = threadIdx.x + e * kThreads;
-        const int h = idx >> 7;
-        float M = -INFINITY;
-        for (int q = 0; q < num_parts; ++q) M = fmaxf(M, __builtin_nontemporal_load(all_ml + q * 2 * kGroup + h));
-        float L = 0.f, O = 0.f;
-        for (int q = 0; q < num_parts; ++q) {
-            const float f = __builtin_amdgcn_exp2f(__builtin_nontemporal_load(all_ml + q * 2 * kGroup + h) - M);
-            L += __builtin_nontemporal_load(all_ml + q * 2 * kGroup + kGroup + h) * f;
-            O += __builtin_nontemporal_load(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + idx) * f;
-        }
-        out[idx] = __builtin_bit_cast(uint16_t, to_h(O / L));
+        out[idx] = __builtin_bit_cast(uint16_t, to_h(acc[e]));
     }
-    if (threadIdx.x == 0) atomicExch(p.counters + s * kKvHeads + g, 0u);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(p.counters + s * kKvHeads + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void fill_u32_kernel(uint32_t *dst, size_t words, uint32_t value) {
@@ -401,11 +495,12 @@ int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
 
     const dim3 grid(launch.max_parts, kKvHeads, a.num_seqs);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // Waves per workgroup: one 64-token chunk per wave up to 4 waves (the
-    // register budget of a wave allows at most one wave per SIMD); longer
-    // partitions loop over chunks.
+    // One 64-token chunk per wave up to 8 waves (two 8-wave workgroups fit a
+    // CU); longer partitions loop over chunks.
     const uint32_t chunks = launch.partition_tokens / kChunkTokens;
-    if (chunks >= 4) {
+    if (chunks >= 8) {
+        hipLaunchKernelGGL(paged_decode_kernel<8>, grid, dim3(512), 0, st, p);
+    } else if (chunks >= 4) {
         hipLaunchKernelGGL(paged_decode_kernel<4>, grid, dim3(256), 0, st, p);
     } else if (chunks >= 2) {
         hipLaunchKernelGGL(paged_decode_kernel<2>, grid, dim3(128), 0, st, p);

@@ -318,14 +318,12 @@ DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts) {
 }
 
 uint32_t auto_partition(uint32_t num_seqs, uint32_t max_context) {
-    // Largest power-of-two partition (<= 512 tokens) that still gives every
-    // CU of the 256 several workgroups; long batched contexts keep 512.
-    uint32_t p = 512;
-    while (p > 64) {
-        const uint64_t groups = static_cast<uint64_t>(num_seqs) * kKvHeads * ((max_context + p - 1) / p);
-        if (groups >= 1024) break;
-        p /= 2;
-    }
+    // 256-token partitions (4 waves x 64 tokens) keep the partials small and
+    // two workgroups resident per CU; long contexts grow the partition so one
+    // merge never combines more than 64 partitions.
+    uint32_t p = 256;
+    while ((max_context + p - 1) / p > kMaxMergeParts && p < 4096) p *= 2;
+    (void)num_seqs;
     return p;
 }
 

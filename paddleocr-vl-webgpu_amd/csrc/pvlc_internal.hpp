@@ -18,6 +18,7 @@ constexpr uint32_t kRowElems = kKvHeads * kHeadDim;          // one cache row, b
 constexpr uint32_t kBlockHeadElems = kBlockTokens * kHeadDim;  // one (block, head) slab
 constexpr uint32_t kMaxDecoderHeadDim = 128;                   // runtime-core lib.rs:180
 constexpr uint32_t kMaxWebgpuDispatch = 65535;                 // runtime-core lib.rs:187
+constexpr uint32_t kMaxMergeParts = 64;  // split-K partitions one in-kernel merge combines
 
 // Status of a failed call: RuntimeErrorCode in bits 8..15, InvocationErrorCode
 // in bits 0..7; records the message for pvlc_hip_last_error_message().

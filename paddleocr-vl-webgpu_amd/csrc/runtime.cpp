@@ -111,6 +111,9 @@ pvlc_hip_status validate_decode_args(const pvlc_hip_paged_decode_args *a, uint32
     if (partition < 64 || partition > 4096 || partition % 64 != 0)
         return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "partition_tokens must be a multiple of 64 in 64..4096");
     const uint32_t max_parts = (a->max_context + partition - 1) / partition;
+    if (max_parts > kMaxMergeParts)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY,
+                       "max_context / partition_tokens exceeds the 64 partitions one merge combines");
     const DecodeWorkspace layout = decode_workspace_layout(a->num_seqs, max_parts);
     if (a->workspace_bytes < layout.total)
         return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "workspace holds " + std::to_string(a->workspace_bytes) +

@@ -198,7 +198,7 @@ def device_decode(layers, prefix, capacity, seed, rope=True, rotate_query=False,
     q = f16_bits(seed + 7, layers * 2048)
     nk = f16_bits(seed + 8, layers * W)
     nv = f16_bits(seed + 9, layers * W)
-    rows = max(capacity, 1) + 8
+    rows = max(capacity, 1 if positions is None else int(np.max(positions)) + 1) + 8
     cos, sin = pvlc.rope_table(500000.0, rows)
     d_k, d_v, d_q, d_nk, d_nv = to_dev(kp), to_dev(vp), to_dev(q), to_dev(nk), to_dev(nv)
     d_out = torch.zeros(layers * 2048, dtype=torch.int16, device="cuda")
