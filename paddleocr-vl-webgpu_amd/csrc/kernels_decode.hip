@@ -39,8 +39,6 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
 
-constexpr int kChunkTokens = 64;  // tokens a wave holds in registers at once
-constexpr int kTilesPerChunk = kChunkTokens / 16;
 constexpr int kMaxParts = static_cast<int>(kMaxMergeParts);
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -117,18 +115,19 @@ __device__ inline uint32_t block_id(const DecodeParams &p, uint32_t seq, uint32_
     return static_cast<uint32_t>(b);
 }
 
-// Issue the loads of one 64-token chunk starting at token ws.  Tiles at or
+// Issue the loads of one chunk (TILES blocks of 16 tokens) starting at ws.  Tiles at or
 // past part_end re-read the last valid tile (never outside the planes) and
 // are masked by the caller; loading unconditionally keeps the loads of all
 // four tiles back to back.
+template <int TILES>
 __device__ inline void load_chunk(const DecodeParams &p, uint32_t s, uint32_t g, int ws, int part_end, int row,
-                                  int kg, half8_t (&kr)[kTilesPerChunk][4], half4_t (&vr)[kTilesPerChunk][8]) {
+                                  int kg, half8_t (&kr)[TILES][4], half4_t (&vr)[TILES][8]) {
     const int last_tile = (part_end - 1) >> 4;
-    uint32_t blk[kTilesPerChunk];
+    uint32_t blk[TILES];
 #pragma unroll
-    for (int i = 0; i < kTilesPerChunk; ++i) blk[i] = block_id(p, s, static_cast<uint32_t>(min((ws >> 4) + i, last_tile)));
+    for (int i = 0; i < TILES; ++i) blk[i] = block_id(p, s, static_cast<uint32_t>(min((ws >> 4) + i, last_tile)));
 #pragma unroll
-    for (int i = 0; i < kTilesPerChunk; ++i) {
+    for (int i = 0; i < TILES; ++i) {
         const size_t slab = (static_cast<size_t>(blk[i]) * kKvHeads + g) * kBlockHeadElems;
         const uint16_t *kbase = p.key_cache + slab;
         const uint16_t *vbase = p.value_cache + slab;
@@ -141,8 +140,9 @@ __device__ inline void load_chunk(const DecodeParams &p, uint32_t s, uint32_t g,
     }
 }
 
-template <int WAVES>
+template <int WAVES, int TILES>
 __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParams p) {
+    constexpr int kChunkTokens = TILES * 16;  // tokens a wave holds in registers at once
     const uint32_t part = blockIdx.x;
     const uint32_t g = blockIdx.y;  // kv head
     const uint32_t s = blockIdx.z;  // sequence (or layer)
@@ -168,8 +168,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     const int num_parts = (T + P - 1) / P;
 
     // First chunk's keys and values: issued before anything else.
-    half8_t kr[kTilesPerChunk][4];
-    half4_t vr[kTilesPerChunk][8];
+    half8_t kr[TILES][4];
+    half4_t vr[TILES][8];
     int ws = part_start + wave * kChunkTokens;
     load_chunk(p, s, g, ws, part_end, row, kg, kr, vr);
 
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
         // masked to -inf, but a re-read tile may hold poison rows, and
         // NaN * 0 would reach P.V).
 #pragma unroll
-        for (int i = 0; i < kTilesPerChunk; ++i) {
+        for (int i = 0; i < TILES; ++i) {
             if (ws + i * 16 >= part_end) {
 #pragma unroll
                 for (int c = 0; c < 8; ++c) vr[i][c] = half4_t{};
@@ -254,9 +254,9 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
         }
         // Patch the appended row; zero rows past it (they may hold poison).
         const int ti = append_tile - (ws >> 4);
-        if (ti >= 0 && ti < kTilesPerChunk) {
+        if (ti >= 0 && ti < TILES) {
 #pragma unroll
-            for (int i = 0; i < kTilesPerChunk; ++i) {
+            for (int i = 0; i < TILES; ++i) {
                 if (i != ti) continue;
                 if (row == append_row) {
 #pragma unroll
@@ -278,10 +278,10 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
         }
 
         // Scores: lane holds tokens ws + i*16 + kg*4 + r (r = 0..3) of head `row`.
-        float x[kTilesPerChunk][4];
+        float x[TILES][4];
         float cmax = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < kTilesPerChunk; ++i) {
+        for (int i = 0; i < TILES; ++i) {
             float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb)
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
         }
 
 #pragma unroll
-        for (int i = 0; i < kTilesPerChunk; ++i) {
+        for (int i = 0; i < TILES; ++i) {
             half4_t pa;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -405,14 +405,29 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     __syncthreads();
     if (!sm_last) return;
 
-    // Merge: stage every partition's (max, sum) in LDS, turn them into one
-    // weight per (partition, head), then sum the partial outputs with the
-    // loads of each batch of partitions in flight together.
+    // Merge: the (max, sum) of every partition is staged in LDS (one load
+    // per thread) while the first batch of partial outputs is already in
+    // flight; one weight per (partition, head) then scales the partials.
     const float *all_o = p.part_o + unit * (kGroup * kHeadDim);
     const float *all_ml = p.part_ml + unit * (2 * kGroup);
     __shared__ float sm_ml[kMaxParts * 2 * kGroup];
     __shared__ float sm_w[kMaxParts * kGroup];
     auto ld = [](const float *q) { return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    constexpr int kBatch = 8;
+    float acc[kPerThread];
+    float v[kBatch][kPerThread];
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) acc[e] = 0.f;
+    auto load_batch = [&](int q0) {
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int q = min(q0 + b, num_parts - 1);  // clamped re-reads get weight 0 below
+#pragma unroll
+            for (int e = 0; e < kPerThread; ++e)
+                v[b][e] = ld(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + threadIdx.x + e * kThreads);
+        }
+    };
+    load_batch(0);
     for (int i = threadIdx.x; i < num_parts * 2 * static_cast<int>(kGroup); i += kThreads) sm_ml[i] = ld(all_ml + i);
     __syncthreads();
     if (threadIdx.x < static_cast<int>(kGroup)) {
@@ -429,19 +444,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
         for (int q = 0; q < num_parts; ++q) sm_w[q * kGroup + h] *= inv;
     }
     __syncthreads();
-    float acc[kPerThread];
-#pragma unroll
-    for (int e = 0; e < kPerThread; ++e) acc[e] = 0.f;
-    constexpr int kBatch = 8;
     for (int q0 = 0; q0 < num_parts; q0 += kBatch) {
-        float v[kBatch][kPerThread];
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b)
-#pragma unroll
-            for (int e = 0; e < kPerThread; ++e)
-                v[b][e] = (q0 + b < num_parts)
-                              ? ld(all_o + static_cast<size_t>(q0 + b) * (kGroup * kHeadDim) + threadIdx.x + e * kThreads)
-                              : 0.f;
+        if (q0 > 0) load_batch(q0);
 #pragma unroll
         for (int b = 0; b < kBatch; ++b)
 #pragma unroll
@@ -495,18 +499,19 @@ int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
 
     const dim3 grid(launch.max_parts, kKvHeads, a.num_seqs);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // One 64-token chunk per wave up to 8 waves (two 8-wave workgroups fit a
-    // CU); longer partitions loop over chunks.
-    const uint32_t chunks = launch.partition_tokens / kChunkTokens;
-    if (chunks >= 8) {
-        hipLaunchKernelGGL(paged_decode_kernel<8>, grid, dim3(512), 0, st, p);
-    } else if (chunks >= 4) {
-        hipLaunchKernelGGL(paged_decode_kernel<4>, grid, dim3(256), 0, st, p);
-    } else if (chunks >= 2) {
-        hipLaunchKernelGGL(paged_decode_kernel<2>, grid, dim3(128), 0, st, p);
+    // Workgroup shape from the partition: TILES blocks of 16 tokens per wave
+    // and chunk, WAVES waves; partitions longer than WAVES*TILES*16 loop.
+    const uint32_t P = launch.partition_tokens;
+    const uint32_t tiles = launch.tiles_per_wave;
+#define PVLC_DECODE_LAUNCH(W, TL) hipLaunchKernelGGL((paged_decode_kernel<W, TL>), grid, dim3((W) * 64), 0, st, p)
+    if (tiles == 1) {
+        if (P >= 128) PVLC_DECODE_LAUNCH(8, 1); else PVLC_DECODE_LAUNCH(4, 1);
+    } else if (tiles == 2) {
+        if (P >= 256) PVLC_DECODE_LAUNCH(8, 2); else PVLC_DECODE_LAUNCH(4, 2);
     } else {
-        hipLaunchKernelGGL(paged_decode_kernel<1>, grid, dim3(64), 0, st, p);
+        if (P >= 512) PVLC_DECODE_LAUNCH(8, 4); else if (P >= 256) PVLC_DECODE_LAUNCH(4, 4); else PVLC_DECODE_LAUNCH(2, 4);
     }
+#undef PVLC_DECODE_LAUNCH
     return static_cast<int>(hipGetLastError());
 }
 

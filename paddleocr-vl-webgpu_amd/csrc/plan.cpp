@@ -317,11 +317,21 @@ DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts) {
     return w;
 }
 
+uint32_t auto_tiles_per_wave(uint32_t partition_tokens) {
+#ifdef PVLC_TILES_PER_WAVE
+    (void)partition_tokens;
+    return PVLC_TILES_PER_WAVE;
+#else
+    return partition_tokens >= 512 ? 4 : 2;
+#endif
+}
+
 uint32_t auto_partition(uint32_t num_seqs, uint32_t max_context) {
-    // 256-token partitions (4 waves x 64 tokens) keep the partials small and
-    // two workgroups resident per CU; long contexts grow the partition so one
-    // merge never combines more than 64 partitions.
-    uint32_t p = 256;
+    // 512-token partitions (8 waves x 64 tokens): measured fastest for the
+    // 18-layer 2k-context step on MI355X (fewer partials to merge beats more
+    // workgroups); long contexts grow the partition so one merge never
+    // combines more than 64 partitions.
+    uint32_t p = 512;
     while ((max_context + p - 1) / p > kMaxMergeParts && p < 4096) p *= 2;
     (void)num_seqs;
     return p;

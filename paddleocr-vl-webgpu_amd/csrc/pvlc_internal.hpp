@@ -60,6 +60,7 @@ size_t value_blocked_index(uint32_t token, uint32_t head, uint32_t dim);
 struct DecodeLaunch {
     const pvlc_hip_paged_decode_args *args;
     uint32_t partition_tokens;
+    uint32_t tiles_per_wave;  // 16-token blocks a wave holds per chunk: 1, 2 or 4
     uint32_t max_parts;
     float *part_o;
     float *part_ml;
@@ -81,5 +82,6 @@ struct DecodeWorkspace {
 };
 DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts);
 uint32_t auto_partition(uint32_t num_seqs, uint32_t max_context);
+uint32_t auto_tiles_per_wave(uint32_t partition_tokens);
 
 }  // namespace pvlc

@@ -131,6 +131,7 @@ pvlc_hip_status launch_decode_checked(const pvlc_hip_paged_decode_args *a, void 
     char *ws = static_cast<char *>(a->workspace);
     DecodeLaunch launch{a,
                         partition,
+                        auto_tiles_per_wave(partition),
                         max_parts,
                         reinterpret_cast<float *>(ws + layout.part_o_offset),
                         reinterpret_cast<float *>(ws + layout.part_ml_offset),

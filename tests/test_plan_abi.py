@@ -198,8 +198,8 @@ def test_rope_table_matches_reference_angle_formula():
 
 
 def test_decode_workspace_and_partition_rules():
-    assert pvlc.decode_partition(1, 1025) == 256
-    assert pvlc.decode_partition(18, 2048) == 256
+    assert pvlc.decode_partition(1, 1025) == 512
+    assert pvlc.decode_partition(18, 2048) == 512
     assert pvlc.decode_partition(256, 32768) == 512  # at most 64 partitions per merge
     assert pvlc.decode_partition(1, 131040) == 2048
     assert pvlc.decode_workspace_bytes(18, 2048, 256) % 256 == 0
