@@ -59,6 +59,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=0,
                     help="only run this many steps (no CPU leg), for rocprofv3 runs")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain 256 MiB device copy (the known-size kernel that scales PMC byte counters)")
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
+                    help="2 = headline 18-layer step (default); 3 = paged ragged batch; 4 = causal prefill; "
+                         "5 = long-context split-K batch")
     return ap.parse_args()
 
 
@@ -68,6 +73,12 @@ def main() -> int:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        return calibrate_copy(args)
+    if args.config == 4:
+        return bench_prefill(args)
+    if args.config in (3, 5):
+        return bench_batched(args)
 
     import torch
 
@@ -163,11 +174,15 @@ def main() -> int:
     gbps = step_bytes / (ms_per_step * 1e-3) / 1e9
     warm_gbps = step_bytes / (warm_ms * 1e-3) / 1e9
 
+    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    # runs (scaled by a copy of known size); see the summary beside it.
     traffic = None
-    tpath = os.path.join(REPO, "profiles", "decode18_t2048_traffic.json")
+    tpath = os.path.join(REPO, "profiles", "decode18_t2048_traffic.txt")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch"):
+                    traffic = int(line.split("=")[1])
 
     result = {
         "metric": "decode-attn µs/step + achieved HBM GB/s (% peak), 18 layers, 2k ctx, 1 GPU",
@@ -203,6 +218,144 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(host_q, host_k, host_v, host_nk, host_nv, cos, sin, args.cpu_seconds,
                                               step_bytes, replicas[0]["keep"][5])
     print(json.dumps(result, ensure_ascii=False))
+    return 0
+
+
+def calibrate_copy(args):
+    """Plain device copy of 256 MiB (reads 256 MiB, writes 256 MiB per launch),
+    run under rocprofv3 --pmc to convert FETCH_SIZE / WRITE_SIZE to bytes."""
+    import torch
+
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(max(args.profile_steps, 10)):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": n}))
+    return 0
+
+
+def _timed_launches(torch, stream, k, fn):
+    """HIP-event time (ms) per call of k back-to-back calls of fn(i)."""
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2_000_000 + 40_000 * k))
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(k):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / k
+
+
+def bench_batched(args):
+    """Configs 3 and 5: one decode step (append + GQA) for a ragged batch of
+    sequences over one paged cache with seeded permuted block tables."""
+    import torch
+
+    from __graft_entry__ import load_package
+
+    pvlc = load_package()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    rng = np.random.default_rng(args.config)
+    if args.config == 3:
+        num_seqs = 64
+        lens = rng.integers(256, 8192 + 1, num_seqs)
+        label = "config 3: 64 seqs, T~U[256,8192], 16-token paged blocks, permuted block tables"
+    else:
+        num_seqs = 256
+        lens = np.exp(rng.uniform(np.log(1024), np.log(32768), num_seqs)).astype(np.int64)
+        label = "config 5: 256 seqs, T~logU[1024,32768], 512-token partitions + LSE merge"
+    max_context = int(lens.max())
+    max_blocks = (max_context + 15) // 16
+    need = (lens + 15) // 16
+    num_blocks = int(need.sum())
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    tables = np.zeros((num_seqs, max_blocks), np.int32)
+    off = 0
+    for i in range(num_seqs):
+        tables[i, :need[i]] = perm[off:off + need[i]]
+        off += need[i]
+    gen = torch.Generator(device=dev).manual_seed(args.config)
+    plane = num_blocks * 16 * W
+    kp = torch.randn(plane, generator=gen, device=dev, dtype=torch.float32).half()
+    vp = torch.randn(plane, generator=gen, device=dev, dtype=torch.float32).half()
+    q = torch.randn(num_seqs * 2048, generator=gen, device=dev, dtype=torch.float32).half()
+    nk = torch.randn(num_seqs * W, generator=gen, device=dev, dtype=torch.float32).half()
+    nv = torch.randn(num_seqs * W, generator=gen, device=dev, dtype=torch.float32).half()
+    out = torch.empty(num_seqs * 2048, dtype=torch.float16, device=dev)
+    d_tables = torch.from_numpy(tables).to(dev)
+    d_lens = torch.from_numpy((lens - 1).astype(np.int32)).to(dev)  # rows cached; the step appends one
+    cos, sin = pvlc.rope_table(ROPE_BASE, max_context)
+    d_cos, d_sin = torch.from_numpy(cos.ravel()).to(dev), torch.from_numpy(sin.ravel()).to(dev)
+    part = 512 if args.config == 5 else args.partition
+    wsb = pvlc.decode_workspace_bytes(num_seqs, max_context, part)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    pvlc.workspace_init(ws, wsb, stream)
+    a = pvlc.paged_decode_args(num_seqs=num_seqs, num_blocks=num_blocks, max_blocks_per_seq=max_blocks,
+                               key_cache=kp, value_cache=vp, query=q, new_key=nk, new_value=nv, out=out,
+                               workspace=ws, workspace_bytes=wsb, max_context=max_context, block_tables=d_tables,
+                               cache_lens=d_lens, rope_cos=d_cos, rope_sin=d_sin, rope_rows=max_context,
+                               partition_tokens=part)
+    for _ in range(args.warmup):
+        pvlc.paged_decode_f16(a, stream)
+    ms = _timed_launches(torch, stream, args.steps, lambda i: pvlc.paged_decode_f16(a, stream))
+    total_t = int(lens.sum())
+    step_bytes = 1024 * total_t + num_seqs * 10240
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    print(json.dumps({"metric": "paged batched decode step µs + achieved HBM GB/s", "config": {
+        "workload": label, "num_seqs": num_seqs, "sum_T": total_t, "max_T": max_context,
+        "partition_tokens": part or pvlc.decode_partition(num_seqs, max_context)},
+        "value": round(ms * 1e3, 2), "unit": "µs/step", "steps": args.steps, "warmup": args.warmup,
+        "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "algorithmic_bytes": step_bytes, "device_error_word": pvlc.workspace_error(ws, wsb, stream)},
+        ensure_ascii=False))
+    return 0
+
+
+def bench_prefill(args):
+    """Config 4: causal prefill of 4096 tokens (rotary on Q and K, rows written to
+    the paged cache) -- MFMA-bound."""
+    import torch
+
+    from __graft_entry__ import load_package
+
+    pvlc = load_package()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    n = 4096
+    gen = torch.Generator(device=dev).manual_seed(4)
+    q = (torch.randn(n * 2048, generator=gen, device=dev) * 0.5).half()
+    k = (torch.randn(n * W, generator=gen, device=dev) * 0.5).half()
+    v = (torch.randn(n * W, generator=gen, device=dev) * 0.5).half()
+    nb = n // 16
+    kp = torch.empty(nb * 16 * W, dtype=torch.float16, device=dev)
+    vp = torch.empty_like(kp)
+    out = torch.empty(n * 2048, dtype=torch.float16, device=dev)
+    scratch = torch.empty(n * 2048, dtype=torch.float16, device=dev)
+    cos, sin = pvlc.rope_table(ROPE_BASE, n)
+    d_cos, d_sin = torch.from_numpy(cos.ravel()).to(dev), torch.from_numpy(sin.ravel()).to(dev)
+
+    def call(i):
+        pvlc.paged_prefill_f16(tokens=n, num_blocks=nb, key_cache=kp, value_cache=vp, query=q, key=k, value=v,
+                               out=out, query_scratch=scratch, rope_cos=d_cos, rope_sin=d_sin, rope_rows=n,
+                               stream=stream)
+
+    for i in range(args.warmup):
+        call(i)
+    ms = _timed_launches(torch, stream, args.steps, call)
+    flops = 16 * (n * (n + 1) // 2) * 512
+    tflops = flops / (ms * 1e-3) / 1e12
+    print(json.dumps({"metric": "causal prefill µs + MFMA TFLOP/s (% fp16 dense peak)", "config": {
+        "workload": "config 4: N=4096, 16q/2kv d128 fp16, x0.5, rotary on Q,K, rows written to the paged cache"},
+        "value": round(ms * 1e3, 2), "unit": "µs/call", "steps": args.steps, "warmup": args.warmup,
+        "achieved_tflops": round(tflops, 1), "pct_mfma_peak": round(100 * tflops / 2500.0, 2),
+        "algorithmic_flops": flops, "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0,
+                                                 "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4)}},
+        ensure_ascii=False))
     return 0
 
 

@@ -363,6 +363,7 @@ typedef struct pvlc_hip_paged_prefill_args {
     uint32_t rope_rows;
     const int32_t *positions; /* [N] or NULL = 0..N-1 */
     uint16_t *query_scratch;  /* [N][16][128] fp16: the rotated query */
+    uint32_t *error_word;     /* optional: bit 1 = block id out of range (row skipped), bit 2 = position outside the rope table */
 } pvlc_hip_paged_prefill_args;
 
 /* Causal prefill: rotary on Q and K, write all N K/V rows into the blocked

@@ -143,7 +143,7 @@ class PagedPrefillArgsC(ctypes.Structure):
     _fields_ = [("tokens", _U32), ("num_blocks", _U32), ("block_table", _VP), ("key_cache", _VP),
                 ("value_cache", _VP), ("query", _VP), ("key", _VP), ("value", _VP), ("out", _VP),
                 ("rope_cos", _VP), ("rope_sin", _VP), ("rope_rows", _U32), ("positions", _VP),
-                ("query_scratch", _VP)]
+                ("query_scratch", _VP), ("error_word", _VP)]
 
 
 # Exported symbols with their C signatures (argtypes, restype).
@@ -540,12 +540,12 @@ def paged_decode_f16(args: PagedDecodeArgsC, stream=None) -> None:
 
 def paged_prefill_f16(*, tokens, num_blocks, key_cache, value_cache, query, key, value, out, query_scratch,
                       block_table=None, rope_cos=None, rope_sin=None, rope_rows=0, positions=None,
-                      stream=None) -> None:
+                      error_word=None, stream=None) -> None:
     """Causal prefill with rotary and paged range append
     (replaces decoder_prefill_mrope/kv_append_range/prefill_gqa, wgsl lib.rs:1262-1416)."""
     a = PagedPrefillArgsC(tokens, num_blocks, _ptr(block_table), _ptr(key_cache), _ptr(value_cache), _ptr(query),
                           _ptr(key), _ptr(value), _ptr(out), _ptr(rope_cos), _ptr(rope_sin), rope_rows,
-                          _ptr(positions), _ptr(query_scratch))
+                          _ptr(positions), _ptr(query_scratch), _ptr(error_word))
     _check(lib.pvlc_hip_paged_prefill_f16(ctypes.byref(a), _stream(stream)))
 
 

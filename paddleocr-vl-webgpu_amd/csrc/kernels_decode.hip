@@ -29,15 +29,11 @@
 
 #include <cstdint>
 
+#include "pvlc_device.hpp"
 #include "pvlc_internal.hpp"
 
 namespace pvlc {
 namespace {
-
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-typedef float float4_t __attribute__((ext_vector_type(4)));
-typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kMaxParts = static_cast<int>(kMaxMergeParts);
 constexpr float kLog2e = 1.4426950408889634f;
@@ -67,41 +63,6 @@ struct DecodeParams {
     uint32_t *error_word;
     float scale_log2;   // log2(e)/sqrt(128)
 };
-
-__device__ inline _Float16 to_h(float f) { return static_cast<_Float16>(f); }
-
-// Read a wave-uniform element of a buffer the kernel never writes (block
-// tables, cache lengths, positions) through the constant address space, so
-// it becomes a scalar load that does not wait behind the vector loads.
-__device__ inline int32_t load_const(const int32_t *base, size_t index) {
-    typedef const __attribute__((address_space(4))) int32_t *constant_ptr;
-    return ((constant_ptr)base)[index];
-}
-
-// Rotate-half of 8 consecutive dims [d0, d0+8) of one head row:
-// x'[d] = x[d]*cos + partner*sin with partner = -x[d+64] (d < 64) or x[d-64],
-// exactly the f32 expression of apply_rope_neox / apply_multimodal_rope_f32
-// (cpu-ref lib.rs:459-463, :645-654); each product and the sum are rounded
-// separately (this file is compiled without FP contraction), then RNE to fp16.
-__device__ inline half8_t rotate_chunk(const uint16_t *row, int d0, const float *cos_row, const float *sin_row) {
-    const half8_t x = *reinterpret_cast<const half8_t *>(row + d0);
-    const half8_t y = *reinterpret_cast<const half8_t *>(row + (d0 < 64 ? d0 + 64 : d0 - 64));
-    const float4_t c0 = *reinterpret_cast<const float4_t *>(cos_row + (d0 & 63));
-    const float4_t c1 = *reinterpret_cast<const float4_t *>(cos_row + (d0 & 63) + 4);
-    const float4_t s0 = *reinterpret_cast<const float4_t *>(sin_row + (d0 & 63));
-    const float4_t s1 = *reinterpret_cast<const float4_t *>(sin_row + (d0 & 63) + 4);
-    const float sign = d0 < 64 ? -1.0f : 1.0f;
-    half8_t r;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float c = j < 4 ? c0[j] : c1[j - 4];
-        const float s = j < 4 ? s0[j] : s1[j - 4];
-        const float xc = static_cast<float>(x[j]) * c;
-        const float ps = (sign * static_cast<float>(y[j])) * s;
-        r[j] = to_h(xc + ps);
-    }
-    return r;
-}
 
 // Physical block of (sequence, tile); `tile` is wave-uniform so the table
 // read is a scalar load.
