@@ -343,3 +343,23 @@ def test_normal_generator_statistics_and_determinism():
     assert abs(a.mean()) < 0.01 and abs(a.std() - 1) < 0.01
     h = O.normal_f16(123, 1000, 0.5)
     np.testing.assert_array_equal(h, (a[:1000] * np.float32(0.5)).astype(np.float16).view(np.uint16))
+
+
+def test_write_prefill_kv_is_a_validated_clone():
+    # write_decoder_prefill_kv_f32, lib.rs:976-992: rows copied unchanged, geometry and finiteness checked
+    tokens, kvh, hd = 7, 2, 8
+    k, v = O.normal_f32(51, tokens * kvh * hd), O.normal_f32(52, tokens * kvh * hd)
+    ok, ov = O.write_prefill_kv_f32(k, v, tokens, kvh, hd)
+    np.testing.assert_array_equal(bits(ok), bits(k))
+    np.testing.assert_array_equal(bits(ov), bits(v))
+    with pytest.raises(O.OracleError) as err:
+        O.write_prefill_kv_f32(k[:-1], v, tokens, kvh, hd)
+    assert err.value.code == "DimensionMismatch"
+    bad = v.copy()
+    bad[4] = np.inf
+    with pytest.raises(O.OracleError) as err:
+        O.write_prefill_kv_f32(k, bad, tokens, kvh, hd)
+    assert err.value.code == "NonFiniteInput"
+    with pytest.raises(O.OracleError) as err:
+        O.write_prefill_kv_f32(k, v, 0, kvh, hd)
+    assert err.value.code == "DimensionMismatch"
