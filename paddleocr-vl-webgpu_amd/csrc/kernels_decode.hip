@@ -1,10 +1,10 @@
 // Paged GQA decode for gfx950: fused rotary + KV append + split-K attention
 // with an in-kernel LSE merge.
 //
-// Work unit: one workgroup per (partition, kv head, sequence).  Each wave of
-// the workgroup streams 64-token chunks (4 blocks of 16 tokens) of its kv
-// head's keys and values straight from HBM into registers in MFMA operand
-// order -- the blocked cache layout makes every wave-wide load one contiguous
+// Work unit: one workgroup per (partition, kv head, sequence).  A partition is
+// a whole number of 16-token blocks.  Each wave of the workgroup streams
+// chunks of 1-4 blocks of its kv head's keys and values straight from HBM
+// into registers in MFMA operand order -- the blocked cache layout makes every wave-wide load one contiguous
 // 1 KiB (keys) or 512 B (values) run -- and serves all 8 query heads of the
 // group with matrix instructions:
 //   scores  S[token][head] = K[token][:] . Q[head][:]   v_mfma_f32_16x16x32_f16
@@ -35,7 +35,6 @@
 namespace pvlc {
 namespace {
 
-constexpr int kMaxParts = static_cast<int>(kMaxMergeParts);
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeParams {
@@ -58,7 +57,7 @@ struct DecodeParams {
     uint32_t partition_tokens;
     uint32_t max_parts;
     float *part_o;      // [seq][kv head][part][8 heads][128]
-    float *part_ml;     // [seq][kv head][part][2][8]: max (log2 units) then sum
+    float *part_ml;     // [seq][kv head][part][8 heads][2]: max (log2 units), sum
     uint32_t *counters; // [seq][kv head]
     uint32_t *error_word;
     float scale_log2;   // log2(e)/sqrt(128)
@@ -76,29 +75,31 @@ __device__ inline uint32_t block_id(const DecodeParams &p, uint32_t seq, uint32_
     return static_cast<uint32_t>(b);
 }
 
-// Issue the loads of one chunk (TILES blocks of 16 tokens) starting at ws.  Tiles at or
-// past part_end re-read the last valid tile (never outside the planes) and
-// are masked by the caller; loading unconditionally keeps the loads of all
-// four tiles back to back.
+// Issue the loads of one chunk (TILES blocks of 16 tokens) starting at ws:
+// the keys of every tile first, then the values, so the scores can be
+// computed while the values are still arriving.  Tiles at or past part_end
+// re-read the last valid tile (never outside the planes) and are masked by
+// the caller; loading unconditionally keeps the loads back to back.
 template <int TILES>
 __device__ inline void load_chunk(const DecodeParams &p, uint32_t s, uint32_t g, int ws, int part_end, int row,
                                   int kg, half8_t (&kr)[TILES][4], half4_t (&vr)[TILES][8]) {
     const int last_tile = (part_end - 1) >> 4;
-    uint32_t blk[TILES];
+    size_t slab[TILES];
 #pragma unroll
-    for (int i = 0; i < TILES; ++i) blk[i] = block_id(p, s, static_cast<uint32_t>(min((ws >> 4) + i, last_tile)));
+    for (int i = 0; i < TILES; ++i)
+        slab[i] = (static_cast<size_t>(block_id(p, s, static_cast<uint32_t>(min((ws >> 4) + i, last_tile)))) * kKvHeads +
+                   g) * kBlockHeadElems;
 #pragma unroll
-    for (int i = 0; i < TILES; ++i) {
-        const size_t slab = (static_cast<size_t>(blk[i]) * kKvHeads + g) * kBlockHeadElems;
-        const uint16_t *kbase = p.key_cache + slab;
-        const uint16_t *vbase = p.value_cache + slab;
+    for (int i = 0; i < TILES; ++i)
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
-            kr[i][kb] = *reinterpret_cast<const half8_t *>(kbase + (kb * 4 + kg) * 128 + row * 8);
+            kr[i][kb] = *reinterpret_cast<const half8_t *>(p.key_cache + slab[i] + (kb * 4 + kg) * 128 + row * 8);
+    __builtin_amdgcn_sched_barrier(0);  // keep every key load ahead of the value loads
+#pragma unroll
+    for (int i = 0; i < TILES; ++i)
 #pragma unroll
         for (int c = 0; c < 8; ++c)
-            vr[i][c] = *reinterpret_cast<const half4_t *>(vbase + (c * 16 + row) * 16 + kg * 4);
-    }
+            vr[i][c] = *reinterpret_cast<const half4_t *>(p.value_cache + slab[i] + (c * 16 + row) * 16 + kg * 4);
 }
 
 template <int WAVES, int TILES>
@@ -128,12 +129,6 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     const int part_end = min(part_start + P, T);
     const int num_parts = (T + P - 1) / P;
 
-    // First chunk's keys and values: issued before anything else.
-    half8_t kr[TILES][4];
-    half4_t vr[TILES][8];
-    int ws = part_start + wave * kChunkTokens;
-    load_chunk(p, s, g, ws, part_end, row, kg, kr, vr);
-
     // Rotary position of the appended row (and of the query).
     bool rope = p.rope_cos != nullptr;
     const int pos = p.positions ? load_const(p.positions, s) : cache_len;
@@ -144,52 +139,94 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     const float *cos_row = rope ? p.rope_cos + static_cast<size_t>(pos) * 64 : nullptr;
     const float *sin_row = rope ? p.rope_sin + static_cast<size_t>(pos) * 64 : nullptr;
 
-    // Query as the B operand of the score MFMA: column = query head of the
-    // group (8 real, 8 zero), k = dims kb*32 + kg*8 .. +8.
+    // Small operands are loaded first, unconditionally and before the
+    // key/value stream, so they return ahead of it and every later wait on
+    // them is a partial one.  The query is the B operand of the score MFMA:
+    // column = query head of the group (8 real, 8 zero), k = dims
+    // kb*32 + kg*8 .. +8 (lanes of the zero columns load a real row and
+    // discard it).
+    const uint16_t *qrow = p.query + (static_cast<size_t>(s) * kQueryHeads + g * kGroup + (row & 7)) * kHeadDim;
     half8_t qb[4];
-    {
-        const uint16_t *qrow = p.query + (static_cast<size_t>(s) * kQueryHeads + g * kGroup + row) * kHeadDim;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) qb[kb] = *reinterpret_cast<const half8_t *>(qrow + kb * 32 + kg * 8);
+    // The appended row and the rotary row at its position: lane t holds
+    // dims t and t+64 (the rotate-half pair) and cos/sin of pair t.
+    const size_t new_base = (static_cast<size_t>(s) * kKvHeads + g) * kHeadDim;
+    const uint16_t nk_lo = p.new_key[new_base + lane];
+    const uint16_t nk_hi = p.new_key[new_base + lane + 64];
+    const uint16_t nv_lo = p.new_value[new_base + lane];
+    const uint16_t nv_hi = p.new_value[new_base + lane + 64];
+    // (Without rotary the loads read the new key row as a stand-in, so they
+    // stay unconditional; the values are then replaced by cos 1, sin 0.)
+    const float *cos_src = rope ? cos_row : reinterpret_cast<const float *>(p.new_key + new_base);
+    const float *sin_src = rope ? sin_row : reinterpret_cast<const float *>(p.new_key + new_base);
+    const float rc_raw = cos_src[lane];
+    const float rs_raw = sin_src[lane];
+    const float rc = rope ? rc_raw : 1.0f;
+    const float rs = rope ? rs_raw : 0.0f;
+
+    // First chunk's keys and values (waves past the end of a short partition
+    // re-read the partition's last tile and never use it).
+    half8_t kr[TILES][4];
+    half4_t vr[TILES][8];
+    int ws = part_start + wave * kChunkTokens;
+    load_chunk(p, s, g, ws, part_end, row, kg, kr, vr);
+
+    if (rope && p.rotate_query) {
+        // Rotate-half of the query in place: the partner of chunk kb is
+        // chunk kb^2 of the same lane, and cos/sin of pair i live in lane i.
+        half8_t qr[4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            const int d0 = kb * 32 + kg * 8;
-            if (row < static_cast<int>(kGroup)) {
-                qb[kb] = (rope && p.rotate_query) ? rotate_chunk(qrow, d0, cos_row, sin_row)
-                                                  : *reinterpret_cast<const half8_t *>(qrow + d0);
-            } else {
-                qb[kb] = half8_t{};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int pair = (kb & 1) * 32 + kg * 8 + j;
+                const float c = __shfl(rc, pair);
+                const float sn = __shfl(rs, pair);
+                const float x = static_cast<float>(qb[kb][j]);
+                const float y = static_cast<float>(qb[kb ^ 2][j]);
+                qr[kb][j] = kb < 2 ? to_h(x * c + (-y) * sn) : to_h(x * c + y * sn);
             }
         }
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) qb[kb] = qr[kb];
     }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+        if (row >= static_cast<int>(kGroup)) qb[kb] = half8_t{};
 
-    // The workgroup whose partition holds the appended row rotates the new
-    // key once, writes the new K/V row into the cache, and keeps it in LDS to
-    // stand in for that row of its tile loads (which may see the old row).
+    // Append: the workgroup whose partition holds the appended row rotates
+    // the new key, writes the new K/V row into the cache, and keeps it in LDS
+    // to stand in for that row of the tile loads (which may see the old row).
+    // Rotate-half in f32 exactly as apply_rope_neox (cpu-ref lib.rs:459-463):
+    // x'[d] = x[d]*cos + (-x[d+64])*sin and x'[d+64] = x[d+64]*cos + x[d]*sin,
+    // products rounded separately (no contraction in this file), then RNE to
+    // fp16.
     const int append_tile = cache_len >> 4;
     const int append_row = cache_len & 15;
+    const bool owns_append = (append_tile << 4) >= part_start && (append_tile << 4) < part_end;
     __shared__ uint16_t sm_new_k[kHeadDim];
     __shared__ uint16_t sm_new_v[kHeadDim];
-    const bool owns_append = (append_tile << 4) >= part_start && (append_tile << 4) < part_end;
     if (owns_append) {
-        if (threadIdx.x < 32) {
+        if (wave == 0) {
+            uint16_t k_lo = nk_lo, k_hi = nk_hi;
+            if (rope) {
+                const float x = static_cast<float>(__builtin_bit_cast(_Float16, nk_lo));
+                const float y = static_cast<float>(__builtin_bit_cast(_Float16, nk_hi));
+                k_lo = __builtin_bit_cast(uint16_t, to_h(x * rc + (-y) * rs));
+                k_hi = __builtin_bit_cast(uint16_t, to_h(y * rc + x * rs));
+            }
             const uint32_t blk = block_id(p, s, static_cast<uint32_t>(append_tile));
             const size_t slab = (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems;
-            if (threadIdx.x < 16) {
-                const uint16_t *new_k = p.new_key + (static_cast<size_t>(s) * kKvHeads + g) * kHeadDim;
-                const int d0 = threadIdx.x * 8;
-                const half8_t nk = rope ? rotate_chunk(new_k, d0, cos_row, sin_row)
-                                        : *reinterpret_cast<const half8_t *>(new_k + d0);
-                *reinterpret_cast<half8_t *>(sm_new_k + d0) = nk;
-                *reinterpret_cast<half8_t *>(p.key_cache + slab + threadIdx.x * 128 + append_row * 8) = nk;
-            } else {
-                const uint16_t *new_v = p.new_value + (static_cast<size_t>(s) * kKvHeads + g) * kHeadDim;
-                const int d0 = (threadIdx.x - 16) * 8;
-                // A uint16 vector: scattering elements of a _Float16 vector
-                // with 16-bit stores stored element 0 eight times on gfx950.
-                const u16x8_t nv = *reinterpret_cast<const u16x8_t *>(new_v + d0);
-                *reinterpret_cast<u16x8_t *>(sm_new_v + d0) = nv;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) p.value_cache[slab + (d0 + j) * 16 + append_row] = nv[j];
-            }
+            sm_new_k[lane] = k_lo;
+            sm_new_k[lane + 64] = k_hi;
+            sm_new_v[lane] = nv_lo;
+            sm_new_v[lane + 64] = nv_hi;
+            // key (append_row, d) at (d/8)*128 + append_row*8 + d%8; value at d*16 + append_row
+            p.key_cache[slab + (lane >> 3) * 128 + append_row * 8 + (lane & 7)] = k_lo;
+            p.key_cache[slab + ((lane + 64) >> 3) * 128 + append_row * 8 + (lane & 7)] = k_hi;
+            p.value_cache[slab + lane * 16 + append_row] = nv_lo;
+            p.value_cache[slab + (lane + 64) * 16 + append_row] = nv_hi;
         }
         __syncthreads();  // uniform: owns_append depends on the workgroup only
     }
@@ -203,38 +240,16 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     for (int chunk = 0; ws < part_end; ++chunk, ws += WAVES * kChunkTokens) {
         if (chunk > 0) load_chunk(p, s, g, ws, part_end, row, kg, kr, vr);
 
-        // Zero the values of tiles past the partition (their scores are
-        // masked to -inf, but a re-read tile may hold poison rows, and
-        // NaN * 0 would reach P.V).
-#pragma unroll
-        for (int i = 0; i < TILES; ++i) {
-            if (ws + i * 16 >= part_end) {
-#pragma unroll
-                for (int c = 0; c < 8; ++c) vr[i][c] = half4_t{};
-            }
-        }
-        // Patch the appended row; zero rows past it (they may hold poison).
-        const int ti = append_tile - (ws >> 4);
-        if (ti >= 0 && ti < TILES) {
+        // Patch the appended row of the keys (the tile loads may predate the
+        // append).
+        const int ti = append_tile - (ws >> 4);  // chunk tile holding the appended row
+        if (ti >= 0 && ti < TILES && row == append_row) {
 #pragma unroll
             for (int i = 0; i < TILES; ++i) {
                 if (i != ti) continue;
-                if (row == append_row) {
 #pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
-                        kr[i][kb] = *reinterpret_cast<const half8_t *>(sm_new_k + (kb * 4 + kg) * 8);
-                }
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int r = kg * 4 + j;
-#pragma unroll
-                    for (int c = 0; c < 8; ++c) {
-                        if (r == append_row)
-                            vr[i][c][j] = __builtin_bit_cast(_Float16, sm_new_v[c * 16 + row]);
-                        else if (r > append_row)
-                            vr[i][c][j] = static_cast<_Float16>(0.0f);
-                    }
-                }
+                for (int kb = 0; kb < 4; ++kb)
+                    kr[i][kb] = *reinterpret_cast<const half8_t *>(sm_new_k + (kb * 4 + kg) * 8);
             }
         }
 
@@ -271,6 +286,34 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
             }
         }
 
+        // Values: zero the tiles past the partition and the rows after the
+        // appended one (their weights are 0, but they may hold poison and
+        // NaN * 0 would reach P.V); patch the appended row.
+#pragma unroll
+        for (int i = 0; i < TILES; ++i) {
+            if (ws + i * 16 >= part_end) {
+#pragma unroll
+                for (int c = 0; c < 8; ++c) vr[i][c] = half4_t{};
+            }
+        }
+        if (ti >= 0 && ti < TILES) {
+#pragma unroll
+            for (int i = 0; i < TILES; ++i) {
+                if (i != ti) continue;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = kg * 4 + j;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        if (r == append_row)
+                            vr[i][c][j] = __builtin_bit_cast(_Float16, sm_new_v[c * 16 + row]);
+                        else if (r > append_row)
+                            vr[i][c][j] = static_cast<_Float16>(0.0f);
+                    }
+                }
+            }
+        }
+
 #pragma unroll
         for (int i = 0; i < TILES; ++i) {
             half4_t pa;
@@ -304,34 +347,30 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     }
     __syncthreads();
 
-    constexpr int kPerThread = (kGroup * kHeadDim) / kThreads;
-    float po[kPerThread], pm[kPerThread], pl[kPerThread];
+    // Each thread owns kPer consecutive output elements of one head.
+    constexpr int kPer = (kGroup * kHeadDim) / kThreads;
+    const int e0 = threadIdx.x * kPer;
+    const int h = e0 >> 7, d0 = e0 & 127;
+    float M = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < kPerThread; ++e) {
-        const int idx = threadIdx.x + e * kThreads;
-        const int h = idx >> 7, d = idx & 127;
-        float M = -INFINITY;
+    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][h]);
+    float L = 0.f;
+    float po[kPer];
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][h]);
-        float L = 0.f, O = 0.f;
+    for (int e = 0; e < kPer; ++e) po[e] = 0.f;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) {
-            const float f = __builtin_amdgcn_exp2f(sm_m[w][h] - M);
-            L += sm_l[w][h] * f;
-            O += sm_o[w][h][d] * f;
-        }
-        po[e] = O;
-        pm[e] = M;
-        pl[e] = L;
+    for (int w = 0; w < WAVES; ++w) {
+        const float f = __builtin_amdgcn_exp2f(sm_m[w][h] - M);  // 0 for a wave without tokens
+        L += sm_l[w][h] * f;
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) po[e] += sm_o[w][h][d0 + e] * f;
     }
 
     uint16_t *out = p.out + (static_cast<size_t>(s) * kQueryHeads + g * kGroup) * kHeadDim;
     if (num_parts == 1) {
+        const float inv = 1.0f / L;
 #pragma unroll
-        for (int e = 0; e < kPerThread; ++e) {
-            const int idx = threadIdx.x + e * kThreads;
-            out[idx] = __builtin_bit_cast(uint16_t, to_h(po[e] / pl[e]));
-        }
+        for (int e = 0; e < kPer; ++e) out[e0 + e] = __builtin_bit_cast(uint16_t, to_h(po[e] * inv));
         return;
     }
 
@@ -344,15 +383,13 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     // invalidate the whole L2 of the XCD in every workgroup.)
     const size_t unit = (static_cast<size_t>(s) * kKvHeads + g) * p.max_parts;
     float *part_o = p.part_o + (unit + part) * (kGroup * kHeadDim);
-    float *part_ml = p.part_ml + (unit + part) * (2 * kGroup);
+    float *part_ml = p.part_ml + (unit + part) * (2 * kGroup);  // [head][max, sum]
 #pragma unroll
-    for (int e = 0; e < kPerThread; ++e) {
-        const int idx = threadIdx.x + e * kThreads;
-        __hip_atomic_store(part_o + idx, po[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((idx & 127) == 0) {
-            __hip_atomic_store(part_ml + (idx >> 7), pm[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(part_ml + kGroup + (idx >> 7), pl[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+    for (int e = 0; e < kPer; ++e)
+        __hip_atomic_store(part_o + e0 + e, po[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d0 == 0) {
+        __hip_atomic_store(part_ml + 2 * h, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part_ml + 2 * h + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // Wait for this wave's partial stores to complete (a single-wave
     // workgroup's __syncthreads() emits no wait), then for every wave.
@@ -366,60 +403,46 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     __syncthreads();
     if (!sm_last) return;
 
-    // Merge: the (max, sum) of every partition is staged in LDS (one load
-    // per thread) while the first batch of partial outputs is already in
-    // flight; one weight per (partition, head) then scales the partials.
+    // Merge, per thread and without barriers: each thread loads the (max,
+    // sum) of its head and its elements of every partition, a batch of
+    // partitions at a time, and folds them into a running LSE combination.
     const float *all_o = p.part_o + unit * (kGroup * kHeadDim);
     const float *all_ml = p.part_ml + unit * (2 * kGroup);
-    __shared__ float sm_ml[kMaxParts * 2 * kGroup];
-    __shared__ float sm_w[kMaxParts * kGroup];
     auto ld = [](const float *q) { return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
     constexpr int kBatch = 8;
-    float acc[kPerThread];
-    float v[kBatch][kPerThread];
+    float Mg = -INFINITY, Lg = 0.f, og[kPer];
 #pragma unroll
-    for (int e = 0; e < kPerThread; ++e) acc[e] = 0.f;
-    auto load_batch = [&](int q0) {
+    for (int e = 0; e < kPer; ++e) og[e] = 0.f;
+    for (int q0 = 0; q0 < num_parts; q0 += kBatch) {
+        float mv[kBatch], lv[kBatch], ov[kBatch][kPer];
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) {
             const int q = min(q0 + b, num_parts - 1);  // clamped re-reads get weight 0 below
+            mv[b] = ld(all_ml + q * (2 * kGroup) + 2 * h);
+            lv[b] = ld(all_ml + q * (2 * kGroup) + 2 * h + 1);
 #pragma unroll
-            for (int e = 0; e < kPerThread; ++e)
-                v[b][e] = ld(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + threadIdx.x + e * kThreads);
+            for (int e = 0; e < kPer; ++e) ov[b][e] = ld(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + e0 + e);
         }
-    };
-    load_batch(0);
-    for (int i = threadIdx.x; i < num_parts * 2 * static_cast<int>(kGroup); i += kThreads) sm_ml[i] = ld(all_ml + i);
-    __syncthreads();
-    if (threadIdx.x < static_cast<int>(kGroup)) {
-        const int h = threadIdx.x;
-        float M = -INFINITY;
-        for (int q = 0; q < num_parts; ++q) M = fmaxf(M, sm_ml[q * 2 * kGroup + h]);
-        float L = 0.f;
-        for (int q = 0; q < num_parts; ++q) {
-            const float f = __builtin_amdgcn_exp2f(sm_ml[q * 2 * kGroup + h] - M);
-            sm_w[q * kGroup + h] = f;
-            L += sm_ml[q * 2 * kGroup + kGroup + h] * f;
-        }
-        const float inv = 1.0f / L;
-        for (int q = 0; q < num_parts; ++q) sm_w[q * kGroup + h] *= inv;
-    }
-    __syncthreads();
-    for (int q0 = 0; q0 < num_parts; q0 += kBatch) {
-        if (q0 > 0) load_batch(q0);
+        float Mb = Mg;
 #pragma unroll
         for (int b = 0; b < kBatch; ++b)
+            if (q0 + b < num_parts) Mb = fmaxf(Mb, mv[b]);  // finite: every partition holds a token
+        const float a = __builtin_amdgcn_exp2f(Mg - Mb);   // 0 on the first batch
+        Lg *= a;
 #pragma unroll
-            for (int e = 0; e < kPerThread; ++e) {
-                const int h = (threadIdx.x + e * kThreads) >> 7;
-                acc[e] += (q0 + b < num_parts) ? v[b][e] * sm_w[(q0 + b) * kGroup + h] : 0.f;
-            }
-    }
+        for (int e = 0; e < kPer; ++e) og[e] *= a;
 #pragma unroll
-    for (int e = 0; e < kPerThread; ++e) {
-        const int idx = threadIdx.x + e * kThreads;
-        out[idx] = __builtin_bit_cast(uint16_t, to_h(acc[e]));
+        for (int b = 0; b < kBatch; ++b) {
+            const float w = (q0 + b < num_parts) ? __builtin_amdgcn_exp2f(mv[b] - Mb) : 0.f;
+            Lg += lv[b] * w;
+#pragma unroll
+            for (int e = 0; e < kPer; ++e) og[e] += ov[b][e] * w;
+        }
+        Mg = Mb;
     }
+    const float inv = 1.0f / Lg;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) out[e0 + e] = __builtin_bit_cast(uint16_t, to_h(og[e] * inv));
     if (threadIdx.x == 0)
         __hip_atomic_store(p.counters + s * kKvHeads + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -461,17 +484,26 @@ int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
     const dim3 grid(launch.max_parts, kKvHeads, a.num_seqs);
     hipStream_t st = static_cast<hipStream_t>(stream);
     // Workgroup shape from the partition: TILES blocks of 16 tokens per wave
-    // and chunk, WAVES waves; partitions longer than WAVES*TILES*16 loop.
-    const uint32_t P = launch.partition_tokens;
+    // and chunk, and the fewest of 2, 4 or 8 waves that cover the partition
+    // in one chunk; partitions longer than 8 waves x TILES blocks loop.
+    const uint32_t part_tiles = (launch.partition_tokens + kBlockTokens - 1) / kBlockTokens;
     const uint32_t tiles = launch.tiles_per_wave;
+    const uint32_t need = (part_tiles + tiles - 1) / tiles;
+    const uint32_t waves = need <= 2 ? 2 : (need <= 4 ? 4 : 8);
 #define PVLC_DECODE_LAUNCH(W, TL) hipLaunchKernelGGL((paged_decode_kernel<W, TL>), grid, dim3((W) * 64), 0, st, p)
-    if (tiles == 1) {
-        if (P >= 128) PVLC_DECODE_LAUNCH(8, 1); else PVLC_DECODE_LAUNCH(4, 1);
-    } else if (tiles == 2) {
-        if (P >= 256) PVLC_DECODE_LAUNCH(8, 2); else PVLC_DECODE_LAUNCH(4, 2);
-    } else {
-        if (P >= 512) PVLC_DECODE_LAUNCH(8, 4); else if (P >= 256) PVLC_DECODE_LAUNCH(4, 4); else PVLC_DECODE_LAUNCH(2, 4);
+#define PVLC_DECODE_WAVES(TL)                                   \
+    do {                                                        \
+        if (waves == 2) PVLC_DECODE_LAUNCH(2, TL);              \
+        else if (waves == 4) PVLC_DECODE_LAUNCH(4, TL);         \
+        else PVLC_DECODE_LAUNCH(8, TL);                         \
+    } while (0)
+    switch (tiles) {
+        case 1: PVLC_DECODE_WAVES(1); break;
+        case 2: PVLC_DECODE_WAVES(2); break;
+        case 3: PVLC_DECODE_WAVES(3); break;
+        default: PVLC_DECODE_WAVES(4); break;
     }
+#undef PVLC_DECODE_WAVES
 #undef PVLC_DECODE_LAUNCH
     return static_cast<int>(hipGetLastError());
 }

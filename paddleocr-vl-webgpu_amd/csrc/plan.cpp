@@ -318,23 +318,53 @@ DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts) {
 }
 
 uint32_t auto_tiles_per_wave(uint32_t partition_tokens) {
-#ifdef PVLC_TILES_PER_WAVE
-    (void)partition_tokens;
-    return PVLC_TILES_PER_WAVE;
-#else
-    return partition_tokens >= 512 ? 4 : 2;
-#endif
+    // Single-shot partitions (at most 8 waves x 4 tiles) give each wave the
+    // fewest tiles that cover the partition with 8 waves; longer partitions
+    // loop over 8 waves x 4 tiles.
+    const uint32_t tiles = (partition_tokens + kBlockTokens - 1) / kBlockTokens;
+    if (tiles > kSingleShotTiles) return 4;
+    return (tiles + 7) / 8;
 }
 
-uint32_t auto_partition(uint32_t num_seqs, uint32_t max_context) {
-    // 512-token partitions (8 waves x 64 tokens): measured fastest for the
-    // 18-layer 2k-context step on MI355X (fewer partials to merge beats more
-    // workgroups); long contexts grow the partition so one merge never
-    // combines more than 64 partitions.
+uint32_t balanced_parts(uint32_t num_seqs) {
+    const uint64_t units = static_cast<uint64_t>(num_seqs) * kKvHeads;
+    const uint64_t parts = kTargetWorkgroups / units;
+    return static_cast<uint32_t>(parts < 1 ? 1 : (parts > kMaxBalancedParts ? kMaxBalancedParts : parts));
+}
+
+uint32_t single_shot_partition(uint32_t num_seqs, uint32_t context) {
+    // Split every (sequence, kv head) into the same number of partitions so
+    // that about one workgroup per compute unit covers the whole step in one
+    // round, each partition a whole number of 16-token tiles.
+    // Partitions are rounded up to whole waves (1, 2, 4 or a multiple of 8
+    // tiles, so no wave of a full partition idles); the last partition of
+    // each sequence is then the short one.
+    const uint32_t tiles = (context + kBlockTokens - 1) / kBlockTokens;
+    const uint32_t parts = balanced_parts(num_seqs);
+    uint32_t part_tiles = (tiles + parts - 1) / parts;
+    if (part_tiles > 8) part_tiles = (part_tiles + 7) / 8 * 8;
+    else if (part_tiles > 4) part_tiles = 8;
+    else if (part_tiles == 3) part_tiles = 4;
+    return part_tiles <= kSingleShotTiles ? part_tiles * kBlockTokens : 0;
+}
+
+uint32_t auto_partition(uint32_t num_seqs, uint32_t context) {
+    if (const uint32_t p = single_shot_partition(num_seqs, context)) return p;
+    // Streaming regime: 512-token partitions, doubled while one merge would
+    // combine more than 64 partitions.
     uint32_t p = 512;
-    while ((max_context + p - 1) / p > kMaxMergeParts && p < 4096) p *= 2;
-    (void)num_seqs;
+    while ((context + p - 1) / p > kMaxMergeParts && p < 4096) p *= 2;
     return p;
+}
+
+uint32_t auto_workspace_parts(uint32_t num_seqs, uint32_t max_context) {
+    // Any automatic launch with cache lengths up to max_context fits: a
+    // single-shot launch uses at most balanced_parts partitions, a streaming
+    // launch the partition of max_context.
+    const uint32_t p = auto_partition(num_seqs, max_context);
+    const uint32_t parts = (max_context + p - 1) / p;
+    const uint32_t balanced = balanced_parts(num_seqs);
+    return parts > balanced ? parts : balanced;
 }
 
 }  // namespace pvlc

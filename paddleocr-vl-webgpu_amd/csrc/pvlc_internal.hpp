@@ -19,6 +19,12 @@ constexpr uint32_t kBlockHeadElems = kBlockTokens * kHeadDim;  // one (block, he
 constexpr uint32_t kMaxDecoderHeadDim = 128;                   // runtime-core lib.rs:180
 constexpr uint32_t kMaxWebgpuDispatch = 65535;                 // runtime-core lib.rs:187
 constexpr uint32_t kMaxMergeParts = 64;  // split-K partitions one in-kernel merge combines
+// Automatic partitioning: workgroups one launch aims to keep resident (one
+// per MI355X compute unit), the most tiles one workgroup covers without
+// looping (8 waves x 4 tiles), and the most partitions of the balanced rule.
+constexpr uint32_t kTargetWorkgroups = 256;
+constexpr uint32_t kSingleShotTiles = 32;
+constexpr uint32_t kMaxBalancedParts = 16;
 
 // Status of a failed call: RuntimeErrorCode in bits 8..15, InvocationErrorCode
 // in bits 0..7; records the message for pvlc_hip_last_error_message().
@@ -60,7 +66,7 @@ size_t value_blocked_index(uint32_t token, uint32_t head, uint32_t dim);
 struct DecodeLaunch {
     const pvlc_hip_paged_decode_args *args;
     uint32_t partition_tokens;
-    uint32_t tiles_per_wave;  // 16-token blocks a wave holds per chunk: 1, 2 or 4
+    uint32_t tiles_per_wave;  // 16-token blocks a wave holds per chunk: 1..4
     uint32_t max_parts;
     float *part_o;
     float *part_ml;
@@ -81,7 +87,15 @@ struct DecodeWorkspace {
     size_t part_o_offset, part_ml_offset, counters_offset, error_offset, total;
 };
 DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts);
-uint32_t auto_partition(uint32_t num_seqs, uint32_t max_context);
+// Partition rules: balanced_parts is the partition count per (sequence, kv
+// head) of the single-shot rule; single_shot_partition returns 0 when a
+// partition would exceed kSingleShotTiles; auto_partition falls back to
+// 512-token (or longer) streaming partitions; auto_workspace_parts bounds the
+// partitions of every automatic launch up to max_context.
+uint32_t balanced_parts(uint32_t num_seqs);
+uint32_t single_shot_partition(uint32_t num_seqs, uint32_t context);
+uint32_t auto_partition(uint32_t num_seqs, uint32_t context);
+uint32_t auto_workspace_parts(uint32_t num_seqs, uint32_t max_context);
 uint32_t auto_tiles_per_wave(uint32_t partition_tokens);
 
 }  // namespace pvlc

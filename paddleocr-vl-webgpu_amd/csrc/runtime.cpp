@@ -46,8 +46,6 @@ struct pvlc_hip_kv_session {
     uint16_t *attention = nullptr;      // device: 16*128 fp16
     void *workspace = nullptr;
     size_t workspace_bytes = 0;
-    uint32_t partition = 0;
-    uint32_t max_parts = 0;
     uint16_t *host_staging = nullptr;  // pinned: operands in, attention out
 };
 
@@ -107,13 +105,28 @@ pvlc_hip_status validate_decode_args(const pvlc_hip_paged_decode_args *a, uint32
     if (!a->cache_lens && a->uniform_cache_len + 1ull > a->max_context)
         return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "uniform cache length leaves no append row");
     if (a->num_seqs > 65535u) return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "num_seqs exceeds 65535");
-    uint32_t partition = a->partition_tokens ? a->partition_tokens : auto_partition(a->num_seqs, a->max_context);
-    if (partition < 64 || partition > 4096 || partition % 64 != 0)
-        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "partition_tokens must be a multiple of 64 in 64..4096");
-    const uint32_t max_parts = (a->max_context + partition - 1) / partition;
+    uint32_t partition = a->partition_tokens;
+    if (partition != 0) {
+        if (partition < kBlockTokens || partition > 4096 || partition % kBlockTokens != 0)
+            return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY,
+                           "partition_tokens must be a multiple of 16 in 16..4096");
+        if ((a->max_context + partition - 1) / partition > kMaxMergeParts)
+            return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY,
+                           "max_context / partition_tokens exceeds the 64 partitions one merge combines");
+    } else {
+        partition = auto_partition(a->num_seqs, a->max_context);
+        // A uniform cache length is known here: balance the partitions for
+        // the rows actually attended when they fit one round.
+        if (!a->cache_lens) {
+            if (const uint32_t p = single_shot_partition(a->num_seqs, a->uniform_cache_len + 1)) partition = p;
+        }
+    }
+    // Grid partitions: the attended rows bound them when they are uniform.
+    const uint32_t rows = a->cache_lens ? a->max_context : a->uniform_cache_len + 1;
+    const uint32_t max_parts = (rows + partition - 1) / partition;
     if (max_parts > kMaxMergeParts)
         return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY,
-                       "max_context / partition_tokens exceeds the 64 partitions one merge combines");
+                       "the context needs more than the 64 partitions one merge combines");
     const DecodeWorkspace layout = decode_workspace_layout(a->num_seqs, max_parts);
     if (a->workspace_bytes < layout.total)
         return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "workspace holds " + std::to_string(a->workspace_bytes) +
@@ -152,9 +165,9 @@ pvlc_hip_status create_session(pvlc_hip_runtime *rt, const pvlc_hip_kv_session_p
     s->plan = plan;
     s->cache_tokens = plan.initial_cache_tokens;
     s->num_blocks = (plan.cache_capacity + kBlockTokens - 1) / kBlockTokens;
-    s->partition = auto_partition(1, plan.cache_capacity);
-    s->max_parts = (plan.cache_capacity + s->partition - 1) / s->partition;
-    s->workspace_bytes = decode_workspace_layout(1, s->max_parts).total;
+    // Steps use the automatic (per-length balanced) partition; the workspace
+    // holds the most partitions any automatic launch up to capacity uses.
+    s->workspace_bytes = decode_workspace_layout(1, auto_workspace_parts(1, plan.cache_capacity)).total;
     const size_t plane_elems = static_cast<size_t>(s->num_blocks) * kBlockTokens * kRowElems;
 
     auto cleanup = [&](pvlc_hip_status st) {
@@ -230,7 +243,7 @@ pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_oper
     a.new_key = s->step_operands + kQueryElems;
     a.new_value = s->step_operands + kQueryElems + kRowElems;
     a.out = s->attention;
-    a.partition_tokens = s->partition;
+    a.partition_tokens = 0;
     a.workspace = s->workspace;
     a.workspace_bytes = s->workspace_bytes;
     if (pvlc_hip_status st = launch_decode_checked(&a, rt->stream)) return st;
@@ -459,9 +472,9 @@ uint32_t pvlc_hip_paged_decode_partition(uint32_t num_seqs, uint32_t max_context
 
 size_t pvlc_hip_paged_decode_workspace_bytes(uint32_t num_seqs, uint32_t max_context, uint32_t partition_tokens) {
     if (num_seqs == 0 || max_context == 0) return 0;
-    const uint32_t p = partition_tokens ? partition_tokens : auto_partition(num_seqs, max_context);
-    if (p < 64 || p % 64 != 0) return 0;
-    return decode_workspace_layout(num_seqs, (max_context + p - 1) / p).total;
+    if (partition_tokens == 0) return decode_workspace_layout(num_seqs, auto_workspace_parts(num_seqs, max_context)).total;
+    if (partition_tokens % kBlockTokens != 0) return 0;
+    return decode_workspace_layout(num_seqs, (max_context + partition_tokens - 1) / partition_tokens).total;
 }
 
 pvlc_hip_status pvlc_hip_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {

@@ -245,7 +245,7 @@ def test_config1_rotary_append_at_1024():
     check_device_layers(r, 1, 1024, label="config1")
 
 
-@pytest.mark.parametrize("partition", [0, 64, 128, 256, 512, 1024])
+@pytest.mark.parametrize("partition", [0, 48, 64, 128, 256, 304, 336, 512, 1024])
 def test_config2_18_layers_at_2048(partition):
     log(f"case: config 2 step (18 layers, T=2048, partition={partition})")
     r = device_decode(18, 2047, 2304, seed=600, partition=partition)
@@ -323,7 +323,7 @@ def paged_case(num_seqs, lo, hi, seed, partition=0, log_uniform=False):
         check_close(widen(out[s * 2048:(s + 1) * 2048]), want, f"paged seq {s} T={n + 1}")
 
 
-@pytest.mark.parametrize("partition", [0, 64, 512])
+@pytest.mark.parametrize("partition", [0, 64, 80, 512])
 def test_paged_ragged_batch(partition):
     log(f"case: paged ragged 12 seqs partition={partition}")
     paged_case(12, 1, 3000, seed=900 + partition, partition=partition)

@@ -198,12 +198,53 @@ def test_rope_table_matches_reference_angle_formula():
 
 
 def test_decode_workspace_and_partition_rules():
-    assert pvlc.decode_partition(1, 1025) == 512
-    assert pvlc.decode_partition(18, 2048) == 512
-    assert pvlc.decode_partition(256, 32768) == 512  # at most 64 partitions per merge
+    # balanced single-shot partitions: about 256 workgroups (one per compute unit) in one round,
+    # at most 16 partitions per (sequence, kv head), whole 16-token tiles
+    # rounded up to whole waves (1, 2, 4 or a multiple of 8 tiles)
+    assert pvlc.decode_partition(1, 1025) == 128         # 2 units: 5 tiles -> 8, 9 partitions
+    assert pvlc.decode_partition(18, 2048) == 384        # 36 units: 19 tiles -> 24, 6 partitions
+    assert pvlc.decode_partition(64, 512) == 256         # 128 units x 2 partitions of 16 tiles
+    assert pvlc.decode_partition(128, 96) == 128         # 256 units: one partition of 6 tiles -> 8
+    # streaming partitions once one workgroup would need more than 32 tiles
+    assert pvlc.decode_partition(64, 8192) == 512
+    assert pvlc.decode_partition(256, 32768) == 512      # at most 64 partitions per merge
     assert pvlc.decode_partition(1, 131040) == 2048
     assert pvlc.decode_workspace_bytes(18, 2048, 256) % 256 == 0
     assert pvlc.decode_workspace_bytes(18, 2048, 63) == 0
+    assert pvlc.decode_workspace_bytes(18, 2048, 48) > 0
+
+
+def _workspace_status(num_seqs, max_context, cache_len, workspace_bytes, partition=0):
+    """Status of a launch whose only possible validation failure is the workspace size (the launch
+    itself fails without a GPU, after validation)."""
+    blocks = (max_context + 15) // 16
+    args = pvlc.paged_decode_args(num_seqs=num_seqs, num_blocks=num_seqs * blocks, max_blocks_per_seq=blocks,
+                                  key_cache=1, value_cache=1, query=1, new_key=1, new_value=1, out=1,
+                                  workspace=1, workspace_bytes=workspace_bytes, max_context=max_context,
+                                  uniform_cache_len=cache_len, partition_tokens=partition)
+    try:
+        pvlc.paged_decode_f16(args)
+    except pvlc.PvlcHipError as e:
+        return e.code, e.invocation_code
+    return None
+
+
+@pytest.mark.parametrize("num_seqs,max_context", [(1, 1040), (1, 131040), (18, 2304), (7, 300), (64, 8192),
+                                                  (100, 40), (256, 4096), (2, 70000)])
+def test_auto_workspace_covers_every_uniform_length(num_seqs, max_context):
+    # The workspace sized for max_context holds every automatic launch with a shorter uniform
+    # cache length (those pick balanced partitions for the rows they attend).
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("this check relies on the launch failing without a GPU")
+    wsb = pvlc.decode_workspace_bytes(num_seqs, max_context, 0)
+    for t in sorted({1, 2, 16, 17, 33, 100, 511, 1000, 1025, 2047, 4097, max_context // 3, max_context}):
+        if t > max_context:
+            continue
+        st = _workspace_status(num_seqs, max_context, t - 1, wsb)
+        assert st != ("InvalidInvocation", "LengthMismatch"), (num_seqs, max_context, t)
+        assert st != ("InvalidInvocation", "InvalidDecoderGeometry"), (num_seqs, max_context, t)
+    assert _workspace_status(num_seqs, max_context, max_context - 1, 256) == ("InvalidInvocation", "LengthMismatch")
 
 
 def test_device_entry_points_validate_before_touching_the_gpu():
