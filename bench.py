@@ -291,7 +291,7 @@ def bench_batched(args):
     d_lens = torch.from_numpy((lens - 1).astype(np.int32)).to(dev)  # rows cached; the step appends one
     cos, sin = pvlc.rope_table(ROPE_BASE, max_context)
     d_cos, d_sin = torch.from_numpy(cos.ravel()).to(dev), torch.from_numpy(sin.ravel()).to(dev)
-    part = 512 if args.config == 5 else args.partition
+    part = args.partition if args.partition else (512 if args.config == 5 else 0)
     wsb = pvlc.decode_workspace_bytes(num_seqs, max_context, part)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     pvlc.workspace_init(ws, wsb, stream)

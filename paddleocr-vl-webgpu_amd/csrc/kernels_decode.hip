@@ -28,6 +28,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
+#include <vector>
 
 #include "pvlc_device.hpp"
 #include "pvlc_internal.hpp"
@@ -63,32 +65,36 @@ struct DecodeParams {
     float scale_log2;   // log2(e)/sqrt(128)
 };
 
-// Physical block of (sequence, tile); `tile` is wave-uniform so the table
-// read is a scalar load.
-__device__ inline uint32_t block_id(const DecodeParams &p, uint32_t seq, uint32_t tile) {
-    if (p.block_tables == nullptr) return seq * p.max_blocks_per_seq + tile;
-    const int32_t b = load_const(p.block_tables, static_cast<size_t>(seq) * p.max_blocks_per_seq + tile);
-    if (b < 0 || static_cast<uint32_t>(b) >= p.num_blocks) {
-        atomicOr(p.error_word, 2u);
-        return 0;  // clamp: never address outside the planes
-    }
-    return static_cast<uint32_t>(b);
+// Block ids of every tile this wave loads in one partition, one per lane:
+// lane c*TILES + i holds the block of tile i of the wave's chunk c.  Tiles
+// past the partition take the partition's last tile (loaded and masked).
+// An id outside the planes reads block 0 and sets *bad.  One vector load
+// per wave and partition, so it can be issued ahead of the key/value loads
+// (or a whole work item ahead).
+template <int WAVES, int TILES>
+__device__ inline uint32_t wave_tile_ids(const DecodeParams &p, uint32_t s, int part_start, int part_end, int wave,
+                                         bool *bad) {
+    const int lane = threadIdx.x & 63;
+    const int tile = (part_start >> 4) + (lane / TILES) * (WAVES * TILES) + wave * TILES + lane % TILES;
+    const int t = min(tile, (part_end - 1) >> 4);
+    if (p.block_tables == nullptr) return s * p.max_blocks_per_seq + static_cast<uint32_t>(t);
+    const int32_t b = p.block_tables[static_cast<size_t>(s) * p.max_blocks_per_seq + t];
+    const bool out = b < 0 || static_cast<uint32_t>(b) >= p.num_blocks;
+    *bad = *bad || out;
+    return out ? 0u : static_cast<uint32_t>(b);
 }
 
-// Issue the loads of one chunk (TILES blocks of 16 tokens) starting at ws:
-// the keys of every tile first, then the values, so the scores can be
-// computed while the values are still arriving.  Tiles at or past part_end
-// re-read the last valid tile (never outside the planes) and are masked by
-// the caller; loading unconditionally keeps the loads back to back.
+// Issue the loads of chunk c of this wave (TILES blocks of 16 tokens): the
+// keys of every tile first, then the values, so the scores can be computed
+// while the values are still arriving.
 template <int TILES>
-__device__ inline void load_chunk(const DecodeParams &p, uint32_t s, uint32_t g, int ws, int part_end, int row,
-                                  int kg, half8_t (&kr)[TILES][4], half4_t (&vr)[TILES][8]) {
-    const int last_tile = (part_end - 1) >> 4;
+__device__ inline void load_chunk(const DecodeParams &p, uint32_t g, uint32_t ids, int c, int row, int kg,
+                                  half8_t (&kr)[TILES][4], half4_t (&vr)[TILES][8]) {
     size_t slab[TILES];
 #pragma unroll
     for (int i = 0; i < TILES; ++i)
-        slab[i] = (static_cast<size_t>(block_id(p, s, static_cast<uint32_t>(min((ws >> 4) + i, last_tile)))) * kKvHeads +
-                   g) * kBlockHeadElems;
+        slab[i] = (static_cast<size_t>(__builtin_amdgcn_readlane(static_cast<int>(ids), c * TILES + i)) * kKvHeads + g) *
+                  kBlockHeadElems;
 #pragma unroll
     for (int i = 0; i < TILES; ++i)
 #pragma unroll
@@ -98,30 +104,29 @@ __device__ inline void load_chunk(const DecodeParams &p, uint32_t s, uint32_t g,
 #pragma unroll
     for (int i = 0; i < TILES; ++i)
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
-            vr[i][c] = *reinterpret_cast<const half4_t *>(p.value_cache + slab[i] + (c * 16 + row) * 16 + kg * 4);
+        for (int cc = 0; cc < 8; ++cc)
+            vr[i][cc] = *reinterpret_cast<const half4_t *>(p.value_cache + slab[i] + (cc * 16 + row) * 16 + kg * 4);
 }
 
-template <int WAVES, int TILES>
-__global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParams p) {
+// One work item: partition `part` of kv head g of sequence s, whose cache
+// holds cache_len rows before the append (rotary position pos); ids are the
+// wave's tile block ids (wave_tile_ids) and ids_bad whether one of them was
+// out of range.  With DEFER_MERGE the partial is only stored (plain stores)
+// for paged_decode_merge_kernel, launched after this kernel; otherwise the
+// last partition to finish merges in-kernel.  Every return is uniform over
+// the workgroup.  Errors are
+// reported after the key/value loads are consumed, so no conditional memory
+// operation sits among them.
+template <int WAVES, int TILES, bool DEFER_MERGE>
+__device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g, uint32_t part, int cache_len,
+                                   int pos, uint32_t ids, bool ids_bad) {
     constexpr int kChunkTokens = TILES * 16;  // tokens a wave holds in registers at once
-    const uint32_t part = blockIdx.x;
-    const uint32_t g = blockIdx.y;  // kv head
-    const uint32_t s = blockIdx.z;  // sequence (or layer)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int row = lane & 15;  // MFMA row/column index of this lane
     const int kg = lane >> 4;   // MFMA k-group of this lane
     constexpr int kThreads = WAVES * 64;
 
-    const int64_t len_raw = p.cache_lens ? load_const(p.cache_lens, s) : static_cast<int64_t>(p.uniform_cache_len);
-    const int64_t capacity = static_cast<int64_t>(p.max_blocks_per_seq) * 16;
-    const int64_t span = static_cast<int64_t>(p.max_parts) * p.partition_tokens;
-    if (len_raw < 0 || len_raw + 1 > capacity || len_raw + 1 > span) {
-        if (part == 0 && g == 0 && threadIdx.x == 0) atomicOr(p.error_word, 1u);
-        return;
-    }
-    const int cache_len = static_cast<int>(len_raw);
     const int T = cache_len + 1;  // rows attended after the append
     const int P = static_cast<int>(p.partition_tokens);
     const int part_start = static_cast<int>(part) * P;
@@ -131,11 +136,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
 
     // Rotary position of the appended row (and of the query).
     bool rope = p.rope_cos != nullptr;
-    const int pos = p.positions ? load_const(p.positions, s) : cache_len;
-    if (rope && (pos < 0 || static_cast<uint32_t>(pos) >= p.rope_rows)) {
-        if (threadIdx.x == 0) atomicOr(p.error_word, 4u);
-        rope = false;
-    }
+    const bool rope_bad = rope && (pos < 0 || static_cast<uint32_t>(pos) >= p.rope_rows);
+    if (rope_bad) rope = false;
     const float *cos_row = rope ? p.rope_cos + static_cast<size_t>(pos) * 64 : nullptr;
     const float *sin_row = rope ? p.rope_sin + static_cast<size_t>(pos) * 64 : nullptr;
 
@@ -170,7 +172,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     half8_t kr[TILES][4];
     half4_t vr[TILES][8];
     int ws = part_start + wave * kChunkTokens;
-    load_chunk(p, s, g, ws, part_end, row, kg, kr, vr);
+    load_chunk(p, g, ids, 0, row, kg, kr, vr);
 
     if (rope && p.rotate_query) {
         // Rotate-half of the query in place: the partner of chunk kb is
@@ -216,17 +218,25 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
                 k_lo = __builtin_bit_cast(uint16_t, to_h(x * rc + (-y) * rs));
                 k_hi = __builtin_bit_cast(uint16_t, to_h(y * rc + x * rs));
             }
-            const uint32_t blk = block_id(p, s, static_cast<uint32_t>(append_tile));
-            const size_t slab = (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems;
+            // The append block's id was checked with the partition's ids (a
+            // bad one is reported there); the row is then not written.
+            int64_t blk = static_cast<int64_t>(s) * p.max_blocks_per_seq + append_tile;
+            if (p.block_tables) {
+                const int32_t b = load_const(p.block_tables, static_cast<size_t>(s) * p.max_blocks_per_seq + append_tile);
+                blk = (b < 0 || static_cast<uint32_t>(b) >= p.num_blocks) ? -1 : b;
+            }
             sm_new_k[lane] = k_lo;
             sm_new_k[lane + 64] = k_hi;
             sm_new_v[lane] = nv_lo;
             sm_new_v[lane + 64] = nv_hi;
-            // key (append_row, d) at (d/8)*128 + append_row*8 + d%8; value at d*16 + append_row
-            p.key_cache[slab + (lane >> 3) * 128 + append_row * 8 + (lane & 7)] = k_lo;
-            p.key_cache[slab + ((lane + 64) >> 3) * 128 + append_row * 8 + (lane & 7)] = k_hi;
-            p.value_cache[slab + lane * 16 + append_row] = nv_lo;
-            p.value_cache[slab + (lane + 64) * 16 + append_row] = nv_hi;
+            if (blk >= 0) {
+                const size_t slab = (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems;
+                // key (append_row, d) at (d/8)*128 + append_row*8 + d%8; value at d*16 + append_row
+                p.key_cache[slab + (lane >> 3) * 128 + append_row * 8 + (lane & 7)] = k_lo;
+                p.key_cache[slab + ((lane + 64) >> 3) * 128 + append_row * 8 + (lane & 7)] = k_hi;
+                p.value_cache[slab + lane * 16 + append_row] = nv_lo;
+                p.value_cache[slab + (lane + 64) * 16 + append_row] = nv_hi;
+            }
         }
         __syncthreads();  // uniform: owns_append depends on the workgroup only
     }
@@ -238,7 +248,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     for (int c = 0; c < 8; ++c) o[c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     for (int chunk = 0; ws < part_end; ++chunk, ws += WAVES * kChunkTokens) {
-        if (chunk > 0) load_chunk(p, s, g, ws, part_end, row, kg, kr, vr);
+        if (chunk > 0) load_chunk(p, g, ids, chunk, row, kg, kr, vr);
 
         // Patch the appended row of the keys (the tile loads may predate the
         // append).
@@ -329,6 +339,11 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     }
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
+    // Deferred error report: bit 1 = a block id outside the planes (that
+    // block read block 0), bit 2 = rotary position outside the table (no
+    // rotation applied).
+    if (__any(ids_bad) && lane == 0) atomicOr(p.error_word, 2u);
+    if (rope_bad && threadIdx.x == 0) atomicOr(p.error_word, 4u);
 
     // Combine the waves of this partition in LDS.
     __shared__ float sm_m[WAVES][kGroup];
@@ -374,6 +389,20 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
         return;
     }
 
+    const size_t unit = (static_cast<size_t>(s) * kKvHeads + g) * p.max_parts;
+    float *part_o = p.part_o + (unit + part) * (kGroup * kHeadDim);
+    float *part_ml = p.part_ml + (unit + part) * (2 * kGroup);  // [head][max, sum]
+    if constexpr (DEFER_MERGE) {
+        // The kernel boundary orders these stores before the merge kernel.
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) part_o[e0 + e] = po[e];
+        if (d0 == 0) {
+            part_ml[2 * h] = M;
+            part_ml[2 * h + 1] = L;
+        }
+        return;
+    }
+
     // Cross-workgroup hand-off without L2 maintenance: partials, the arrival
     // counter and the merge reads are relaxed agent-scope atomics (sc1), which
     // are coherent across the XCDs' L2s by themselves.  Every store of the
@@ -381,9 +410,6 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     // 0 counts the arrival, which orders the partials before the count.
     // (A C++ release/acquire fence at agent scope would instead write back and
     // invalidate the whole L2 of the XCD in every workgroup.)
-    const size_t unit = (static_cast<size_t>(s) * kKvHeads + g) * p.max_parts;
-    float *part_o = p.part_o + (unit + part) * (kGroup * kHeadDim);
-    float *part_ml = p.part_ml + (unit + part) * (2 * kGroup);  // [head][max, sum]
 #pragma unroll
     for (int e = 0; e < kPer; ++e)
         __hip_atomic_store(part_o + e0 + e, po[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -447,12 +473,238 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
         __hip_atomic_store(p.counters + s * kKvHeads + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Cache length of sequence s if it is valid for this launch (one row to
+// append, inside the block table and the partitions of the workspace), else -1.
+__device__ inline int64_t checked_cache_len(const DecodeParams &p, int64_t len) {
+    const int64_t capacity = static_cast<int64_t>(p.max_blocks_per_seq) * 16;
+    const int64_t span = static_cast<int64_t>(p.max_parts) * p.partition_tokens;
+    return (len < 0 || len + 1 > capacity || len + 1 > span) ? -1 : len;
+}
+
+// Grid (partition, kv head, sequence): sequences of one uniform length, or
+// ragged lengths when there are too many sequences for the ragged kernel.
+template <int WAVES, int TILES>
+__global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParams p) {
+    const uint32_t part = blockIdx.x;
+    const uint32_t g = blockIdx.y;  // kv head
+    const uint32_t s = blockIdx.z;  // sequence (or layer)
+    const int64_t len = checked_cache_len(
+        p, p.cache_lens ? load_const(p.cache_lens, s) : static_cast<int64_t>(p.uniform_cache_len));
+    if (len < 0) {
+        if (part == 0 && g == 0 && threadIdx.x == 0) atomicOr(p.error_word, 1u);
+        return;
+    }
+    const int cache_len = static_cast<int>(len);
+    const int P = static_cast<int>(p.partition_tokens);
+    const int part_start = static_cast<int>(part) * P;
+    if (part_start > cache_len) return;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    bool bad = false;
+    const uint32_t ids = wave_tile_ids<WAVES, TILES>(p, s, part_start, min(part_start + P, cache_len + 1), wave, &bad);
+    const int pos = p.positions ? load_const(p.positions, s) : cache_len;
+    decode_item<WAVES, TILES, false>(p, s, g, part, cache_len, pos, ids, bad);
+}
+
+// Exclusive scan of one int per thread over the workgroup; *total receives
+// the sum.
+template <int kThreads>
+__device__ inline int workgroup_exclusive_scan(int v, int *sm_wave_sums, int *total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) sm_wave_sums[wave] = x;
+    __syncthreads();
+    int before = 0, sum = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) {
+        const int t = sm_wave_sums[w];
+        before += w < wave ? t : 0;
+        sum += t;
+    }
+    __syncthreads();
+    *total = sum;
+    return before + x - v;
+}
+
+// Persistent grid for ragged lengths and long contexts: every workgroup
+// reads the cache lengths (and positions) once into LDS, numbers the (sequence, partition,
+// kv head) items that hold rows, and walks items blockIdx.x,
+// blockIdx.x + gridDim.x, ...  Sequences with fewer partitions launch no
+// empty workgroups, so every compute unit stays on real work, and the block
+// ids of the next item are loaded while the current one runs.
+template <int WAVES, int TILES>
+__global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(DecodeParams p, uint32_t num_seqs) {
+    constexpr int kThreads = WAVES * 64;
+    __shared__ int sm_first[kMaxRaggedSeqs + 1];  // first item (per kv head) of each sequence
+    __shared__ int sm_len[kMaxRaggedSeqs];        // cache length, -1 if invalid
+    __shared__ int sm_pos[kMaxRaggedSeqs];        // rotary position of the appended row
+    __shared__ int sm_wave_sums[WAVES];
+    const int P = static_cast<int>(p.partition_tokens);
+    const int n = static_cast<int>(num_seqs);
+    const int per = (n + kThreads - 1) / kThreads;
+    const int i0 = static_cast<int>(threadIdx.x) * per;
+    int local = 0;
+    for (int i = i0; i < min(i0 + per, n); ++i) {
+        const int64_t len =
+            checked_cache_len(p, p.cache_lens ? p.cache_lens[i] : static_cast<int64_t>(p.uniform_cache_len));
+        if (len < 0 && blockIdx.x == 0) atomicOr(p.error_word, 1u);
+        const int parts = len < 0 ? 0 : static_cast<int>((len + P) / P);  // ceil((len + 1) / P)
+        sm_len[i] = static_cast<int>(len);
+        sm_pos[i] = p.positions ? p.positions[i] : static_cast<int>(len);
+        sm_first[i + 1] = parts;
+        local += parts;
+    }
+    int total = 0;
+    int run = workgroup_exclusive_scan<kThreads>(local, sm_wave_sums, &total);
+    for (int i = i0; i < min(i0 + per, n); ++i) {
+        run += sm_first[i + 1];
+        sm_first[i + 1] = run;
+    }
+    if (threadIdx.x == 0) sm_first[0] = 0;
+    __syncthreads();
+
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    // Item k (per kv head) lies in the last sequence s with sm_first[s] <= k
+    // (sequences without partitions share their successor's start).
+    auto locate = [&](int k, uint32_t *s_out, uint32_t *part_out) {
+        int lo = 0, hi = n - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (sm_first[mid] <= k) lo = mid;
+            else hi = mid - 1;
+        }
+        *s_out = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(lo));
+        *part_out = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(k - sm_first[lo]));
+    };
+    const int items = total * static_cast<int>(kKvHeads);
+    int item = blockIdx.x;
+    if (item >= items) return;
+    uint32_t s = 0, part = 0;
+    locate(item >> 1, &s, &part);
+    bool bad = false;
+    uint32_t ids = wave_tile_ids<WAVES, TILES>(p, s, static_cast<int>(part) * P,
+                                               min(static_cast<int>(part + 1) * P, sm_len[s] + 1), wave, &bad);
+    for (;;) {
+        const int next = item + static_cast<int>(gridDim.x);
+        uint32_t s_next = 0, part_next = 0, ids_next = 0;
+        bool bad_next = false;
+        if (next < items) {
+            locate(next >> 1, &s_next, &part_next);
+            ids_next = wave_tile_ids<WAVES, TILES>(p, s_next, static_cast<int>(part_next) * P,
+                                                   min(static_cast<int>(part_next + 1) * P, sm_len[s_next] + 1), wave,
+                                                   &bad_next);
+        }
+        decode_item<WAVES, TILES, true>(p, s, static_cast<uint32_t>(item & 1), part, sm_len[s], sm_pos[s], ids, bad);
+        if (next >= items) break;
+        __syncthreads();  // the next item reuses the workgroup's LDS
+        item = next;
+        s = s_next;
+        part = part_next;
+        ids = ids_next;
+        bad = bad_next;
+    }
+}
+
+// LSE merge of the partials the ragged kernel stored: one workgroup per
+// (kv head, sequence); each thread folds 4 consecutive output elements of one
+// head over every partition, 16 partitions per batch of loads.  Sequences of
+// one partition were written directly by the ragged kernel.
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p) {
+    const uint32_t g = blockIdx.x;
+    const uint32_t s = blockIdx.y;
+    const int64_t len = checked_cache_len(
+        p, p.cache_lens ? load_const(p.cache_lens, s) : static_cast<int64_t>(p.uniform_cache_len));
+    if (len < 0) return;
+    const int P = static_cast<int>(p.partition_tokens);
+    const int num_parts = static_cast<int>((len + P) / P);
+    if (num_parts <= 1) return;
+    const int e0 = threadIdx.x * 4;
+    const int h = e0 >> 7;
+    const size_t unit = (static_cast<size_t>(s) * kKvHeads + g) * p.max_parts;
+    const float *all_o = p.part_o + unit * (kGroup * kHeadDim);
+    const float *all_ml = p.part_ml + unit * (2 * kGroup);
+    constexpr int kBatch = 16;
+    float Mg = -INFINITY, Lg = 0.f;
+    float4_t og = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int q0 = 0; q0 < num_parts; q0 += kBatch) {
+        float mv[kBatch], lv[kBatch];
+        float4_t ov[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int q = min(q0 + b, num_parts - 1);  // clamped re-reads get weight 0 below
+            mv[b] = all_ml[q * (2 * kGroup) + 2 * h];
+            lv[b] = all_ml[q * (2 * kGroup) + 2 * h + 1];
+            ov[b] = *reinterpret_cast<const float4_t *>(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + e0);
+        }
+        float Mb = Mg;
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b)
+            if (q0 + b < num_parts) Mb = fmaxf(Mb, mv[b]);  // finite: every partition holds a token
+        const float a = __builtin_amdgcn_exp2f(Mg - Mb);   // 0 on the first batch
+        Lg *= a;
+        og *= a;
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const float w = (q0 + b < num_parts) ? __builtin_amdgcn_exp2f(mv[b] - Mb) : 0.f;
+            Lg += lv[b] * w;
+            og += ov[b] * w;
+        }
+        Mg = Mb;
+    }
+    const float inv = 1.0f / Lg;
+    uint16_t *out = p.out + (static_cast<size_t>(s) * kQueryHeads + g * kGroup) * kHeadDim + e0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = __builtin_bit_cast(uint16_t, to_h(og[e] * inv));
+}
+
 __global__ void fill_u32_kernel(uint32_t *dst, size_t words, uint32_t value) {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < words) dst[i] = value;
 }
 
 }  // namespace
+
+// Workgroups of `kernel` the current device keeps resident at once (compute
+// units x workgroups per unit), at most max_items; cached per kernel and device.
+uint32_t resident_workgroups(const void *kernel, int threads, uint64_t max_items, int *err) {
+    struct Entry {
+        const void *kernel;
+        int device;
+        uint32_t wgs;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int device = 0;
+    if (hipError_t r = hipGetDevice(&device)) {
+        *err = static_cast<int>(r);
+        return 0;
+    }
+    uint32_t wgs = 0;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (const Entry &c : cache)
+            if (c.kernel == kernel && c.device == device) wgs = c.wgs;
+    }
+    if (wgs == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipError_t r = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device)) {
+            *err = static_cast<int>(r);
+            return 0;
+        }
+        if (hipError_t r = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0)) {
+            *err = static_cast<int>(r);
+            return 0;
+        }
+        wgs = static_cast<uint32_t>(cus * (per_cu > 0 ? per_cu : 1));
+        std::lock_guard<std::mutex> lock(mu);
+        cache.push_back({kernel, device, wgs});
+    }
+    return static_cast<uint32_t>(max_items < wgs ? (max_items ? max_items : 1) : wgs);
+}
 
 int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
     const pvlc_hip_paged_decode_args &a = *launch.args;
@@ -481,15 +733,40 @@ int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
     p.error_word = launch.error_word;
     p.scale_log2 = kLog2e / sqrtf(static_cast<float>(kHeadDim));
 
-    const dim3 grid(launch.max_parts, kKvHeads, a.num_seqs);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // Workgroup shape from the partition: TILES blocks of 16 tokens per wave
-    // and chunk, and the fewest of 2, 4 or 8 waves that cover the partition
-    // in one chunk; partitions longer than 8 waves x TILES blocks loop.
     const uint32_t part_tiles = (launch.partition_tokens + kBlockTokens - 1) / kBlockTokens;
+    int e = 0;
+    // Streaming regime (ragged lengths, or partitions longer than one chunk
+    // of 8 waves): the persistent kernel stores partials and a second kernel
+    // merges them, so no workgroup waits on a cross-workgroup hand-off.  Its
+    // workgroups are 4 waves of 2 tiles (several resident per compute unit).
+    const bool streaming = (a.cache_lens != nullptr || part_tiles > kSingleShotTiles) && a.num_seqs <= kMaxRaggedSeqs;
+    if (streaming) {
+        const uint64_t max_items = static_cast<uint64_t>(launch.max_parts) * kKvHeads * a.num_seqs;
+#define PVLC_RAGGED_LAUNCH(W, TL)                                                                                  \
+    do {                                                                                                           \
+        const uint32_t wgs = resident_workgroups(reinterpret_cast<const void *>(&paged_decode_ragged_kernel<W, TL>), \
+                                                 (W) * 64, max_items, &e);                                         \
+        if (e == 0) {                                                                                              \
+            hipLaunchKernelGGL((paged_decode_ragged_kernel<W, TL>), dim3(wgs), dim3((W) * 64), 0, st, p, a.num_seqs); \
+            hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(kKvHeads, a.num_seqs), dim3(256), 0, st, p);       \
+        }                                                                                                          \
+    } while (0)
+        if (part_tiles >= 8) PVLC_RAGGED_LAUNCH(4, 2);
+        else if (part_tiles >= 4) PVLC_RAGGED_LAUNCH(4, 1);
+        else PVLC_RAGGED_LAUNCH(2, 1);
+#undef PVLC_RAGGED_LAUNCH
+        if (e != 0) return e;
+        return static_cast<int>(hipGetLastError());
+    }
+
+    // Single-shot regime: one workgroup per (partition, kv head, sequence),
+    // TILES blocks of 16 tokens per wave and the fewest of 2, 4 or 8 waves
+    // that cover the partition; the last partition to finish merges.
     const uint32_t tiles = launch.tiles_per_wave;
     const uint32_t need = (part_tiles + tiles - 1) / tiles;
     const uint32_t waves = need <= 2 ? 2 : (need <= 4 ? 4 : 8);
+    const dim3 grid(launch.max_parts, kKvHeads, a.num_seqs);
 #define PVLC_DECODE_LAUNCH(W, TL) hipLaunchKernelGGL((paged_decode_kernel<W, TL>), grid, dim3((W) * 64), 0, st, p)
 #define PVLC_DECODE_WAVES(TL)                                   \
     do {                                                        \

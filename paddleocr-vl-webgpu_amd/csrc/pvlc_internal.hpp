@@ -25,6 +25,9 @@ constexpr uint32_t kMaxMergeParts = 64;  // split-K partitions one in-kernel mer
 constexpr uint32_t kTargetWorkgroups = 256;
 constexpr uint32_t kSingleShotTiles = 32;
 constexpr uint32_t kMaxBalancedParts = 16;
+// Sequences the ragged (persistent) decode kernel numbers in LDS; launches
+// with more ragged sequences use one workgroup per (partition, head, sequence).
+constexpr uint32_t kMaxRaggedSeqs = 2048;
 
 // Status of a failed call: RuntimeErrorCode in bits 8..15, InvocationErrorCode
 // in bits 0..7; records the message for pvlc_hip_last_error_message().
