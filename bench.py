@@ -281,8 +281,14 @@ def bench_batched(args):
         off += need[i]
     gen = torch.Generator(device=dev).manual_seed(args.config)
     plane = num_blocks * 16 * W
-    kp = torch.randn(plane, generator=gen, device=dev, dtype=torch.float32).half()
-    vp = torch.randn(plane, generator=gen, device=dev, dtype=torch.float32).half()
+    # Caches under ~600 MB are rotated over replicas so every step reads HBM,
+    # not the 256 MB Infinity Cache left warm by the previous step.
+    reps = max(1, min(4, -(-600 * 2**20 // (2 * plane * 2))))
+    planes = []
+    for _ in range(reps):
+        kp = torch.randn(plane, generator=gen, device=dev, dtype=torch.float32).half()
+        vp = torch.randn(plane, generator=gen, device=dev, dtype=torch.float32).half()
+        planes.append((kp, vp))
     q = torch.randn(num_seqs * 2048, generator=gen, device=dev, dtype=torch.float32).half()
     nk = torch.randn(num_seqs * W, generator=gen, device=dev, dtype=torch.float32).half()
     nv = torch.randn(num_seqs * W, generator=gen, device=dev, dtype=torch.float32).half()
@@ -295,19 +301,20 @@ def bench_batched(args):
     wsb = pvlc.decode_workspace_bytes(num_seqs, max_context, part)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     pvlc.workspace_init(ws, wsb, stream)
-    a = pvlc.paged_decode_args(num_seqs=num_seqs, num_blocks=num_blocks, max_blocks_per_seq=max_blocks,
-                               key_cache=kp, value_cache=vp, query=q, new_key=nk, new_value=nv, out=out,
-                               workspace=ws, workspace_bytes=wsb, max_context=max_context, block_tables=d_tables,
-                               cache_lens=d_lens, rope_cos=d_cos, rope_sin=d_sin, rope_rows=max_context,
-                               partition_tokens=part)
-    for _ in range(args.warmup):
-        pvlc.paged_decode_f16(a, stream)
-    ms = _timed_launches(torch, stream, args.steps, lambda i: pvlc.paged_decode_f16(a, stream))
+    launches = [pvlc.paged_decode_args(num_seqs=num_seqs, num_blocks=num_blocks, max_blocks_per_seq=max_blocks,
+                                       key_cache=kp, value_cache=vp, query=q, new_key=nk, new_value=nv, out=out,
+                                       workspace=ws, workspace_bytes=wsb, max_context=max_context,
+                                       block_tables=d_tables, cache_lens=d_lens, rope_cos=d_cos, rope_sin=d_sin,
+                                       rope_rows=max_context, partition_tokens=part)
+                for kp, vp in planes]
+    for i in range(args.warmup):
+        pvlc.paged_decode_f16(launches[i % reps], stream)
+    ms = _timed_launches(torch, stream, args.steps, lambda i: pvlc.paged_decode_f16(launches[i % reps], stream))
     total_t = int(lens.sum())
     step_bytes = 1024 * total_t + num_seqs * 10240
     gbps = step_bytes / (ms * 1e-3) / 1e9
     print(json.dumps({"metric": "paged batched decode step µs + achieved HBM GB/s", "config": {
-        "workload": label, "num_seqs": num_seqs, "sum_T": total_t, "max_T": max_context,
+        "workload": label, "num_seqs": num_seqs, "sum_T": total_t, "max_T": max_context, "cache_replicas": reps,
         "partition_tokens": part or pvlc.decode_partition(num_seqs, max_context)},
         "value": round(ms * 1e3, 2), "unit": "µs/step", "steps": args.steps, "warmup": args.warmup,
         "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),

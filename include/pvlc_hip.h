@@ -280,11 +280,13 @@ void pvlc_hip_kv_session_fail_next_step_after_submit(pvlc_hip_kv_session *sessio
  * Device-resident hot path (fp16, caller stream, no allocation, no sync).
  *
  * Blocked KV layout in HBM.  A cache is two planes of 16-token blocks:
- *   key plane   [num_blocks][2 kv heads][16 dim-chunks][16 tokens][8 dims]
+ *   key plane   [num_blocks][2 kv heads][16 dim-chunks][16 token slots][8 dims]
  *   value plane [num_blocks][2 kv heads][128 dims][16 tokens]
  * so key element (block b, head h, token t, dim d) is at
- *   ((b*2 + h)*16 + d/8)*128 + t*8 + d%8
- * and value element at ((b*2 + h)*128 + d)*16 + t (fp16 elements).  Each
+ *   ((b*2 + h)*16 + d/8)*128 + slot(t)*8 + d%8,  slot(t) = t with bits 2 and 3 swapped
+ * and value element at ((b*2 + h)*128 + d)*16 + t (fp16 elements).  (The
+ * slot order lets the decode and prefill kernels read values with 16-byte
+ * loads into 16x16x32 MFMAs.)  Each
  * (block, head) is 4 KiB per plane.  The compact reference planes
  * [tokens][2][128] convert to and from this layout bit-exactly with
  * pvlc_hip_kv_pack_f16 / pvlc_hip_kv_unpack_f16.

@@ -561,10 +561,15 @@ def kv_unpack_f16(key_cache, value_cache, tokens, key_rows, value_rows, num_bloc
                                       _ptr(key_rows), _ptr(value_rows), _stream(stream)))
 
 
+def key_slot(t):
+    """Slot of token t (0..15) inside a 16-token block of the key plane: bits 2 and 3 swapped."""
+    return (t & 3) | ((t & 4) << 1) | ((t & 8) >> 1)
+
+
 def blocked_key_index(token: np.ndarray, head: np.ndarray, dim: np.ndarray) -> np.ndarray:
     """Element offset of key (token, head, dim) in contiguous blocked planes."""
     b, t = token // BLOCK_TOKENS, token % BLOCK_TOKENS
-    return ((b * KV_HEADS + head) * (HEAD_DIM // 8) + dim // 8) * (BLOCK_TOKENS * 8) + t * 8 + dim % 8
+    return ((b * KV_HEADS + head) * (HEAD_DIM // 8) + dim // 8) * (BLOCK_TOKENS * 8) + key_slot(t) * 8 + dim % 8
 
 
 def blocked_value_index(token: np.ndarray, head: np.ndarray, dim: np.ndarray) -> np.ndarray:

@@ -84,28 +84,38 @@ __device__ inline uint32_t wave_tile_ids(const DecodeParams &p, uint32_t s, int 
     return out ? 0u : static_cast<uint32_t>(b);
 }
 
-// Issue the loads of chunk c of this wave (TILES blocks of 16 tokens): the
-// keys of every tile first, then the values, so the scores can be computed
-// while the values are still arriving.
-template <int TILES>
+// Issue the loads of chunk c of this wave: PAIRS pairs of 16-token tiles.
+// Keys: score MFMA h of pair j takes rows 0-7 from the pair's first tile and
+// rows 8-15 from its second, key slots h*8 .. h*8+7 (see key_slot).  Values:
+// k-groups 0-1 read the first tile, 2-3 the second, 8 consecutive tokens
+// (16 bytes) each.  Every key load is issued before the value loads, so the
+// scores can be computed while the values are still arriving.
+template <int PAIRS>
 __device__ inline void load_chunk(const DecodeParams &p, uint32_t g, uint32_t ids, int c, int row, int kg,
-                                  half8_t (&kr)[TILES][4], half4_t (&vr)[TILES][8]) {
-    size_t slab[TILES];
+                                  half8_t (&kr)[PAIRS][2][4], half8_t (&vr)[PAIRS][8]) {
+    const uint16_t *kbase[PAIRS];
+    const uint16_t *vbase[PAIRS];
 #pragma unroll
-    for (int i = 0; i < TILES; ++i)
-        slab[i] = (static_cast<size_t>(__builtin_amdgcn_readlane(static_cast<int>(ids), c * TILES + i)) * kKvHeads + g) *
-                  kBlockHeadElems;
+    for (int j = 0; j < PAIRS; ++j) {
+        const int t0 = c * 2 * PAIRS + 2 * j;
+        const size_t b0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ids), t0));
+        const size_t b1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ids), t0 + 1));
+        kbase[j] = p.key_cache + ((row < 8 ? b0 : b1) * kKvHeads + g) * kBlockHeadElems;
+        vbase[j] = p.value_cache + ((kg < 2 ? b0 : b1) * kKvHeads + g) * kBlockHeadElems;
+    }
 #pragma unroll
-    for (int i = 0; i < TILES; ++i)
+    for (int j = 0; j < PAIRS; ++j)
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-            kr[i][kb] = *reinterpret_cast<const half8_t *>(p.key_cache + slab[i] + (kb * 4 + kg) * 128 + row * 8);
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+                kr[j][h][kb] = *reinterpret_cast<const half8_t *>(kbase[j] + (kb * 4 + kg) * 128 + (h * 8 + (row & 7)) * 8);
     __builtin_amdgcn_sched_barrier(0);  // keep every key load ahead of the value loads
 #pragma unroll
-    for (int i = 0; i < TILES; ++i)
+    for (int j = 0; j < PAIRS; ++j)
 #pragma unroll
         for (int cc = 0; cc < 8; ++cc)
-            vr[i][cc] = *reinterpret_cast<const half4_t *>(p.value_cache + slab[i] + (cc * 16 + row) * 16 + kg * 4);
+            vr[j][cc] = *reinterpret_cast<const half8_t *>(vbase[j] + (cc * 16 + row) * 16 + (kg & 1) * 8);
 }
 
 // One work item: partition `part` of kv head g of sequence s, whose cache
@@ -117,10 +127,11 @@ __device__ inline void load_chunk(const DecodeParams &p, uint32_t g, uint32_t id
 // the workgroup.  Errors are
 // reported after the key/value loads are consumed, so no conditional memory
 // operation sits among them.
-template <int WAVES, int TILES, bool DEFER_MERGE>
+template <int WAVES, int PAIRS, bool DEFER_MERGE>
 __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g, uint32_t part, int cache_len,
                                    int pos, uint32_t ids, bool ids_bad) {
-    constexpr int kChunkTokens = TILES * 16;  // tokens a wave holds in registers at once
+    constexpr int kChunkTiles = 2 * PAIRS;         // 16-token tiles a wave holds in registers at once
+    constexpr int kChunkTokens = kChunkTiles * 16;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int row = lane & 15;  // MFMA row/column index of this lane
@@ -169,10 +180,10 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
 
     // First chunk's keys and values (waves past the end of a short partition
     // re-read the partition's last tile and never use it).
-    half8_t kr[TILES][4];
-    half4_t vr[TILES][8];
+    half8_t kr[PAIRS][2][4];
+    half8_t vr[PAIRS][8];
     int ws = part_start + wave * kChunkTokens;
-    load_chunk(p, g, ids, 0, row, kg, kr, vr);
+    load_chunk<PAIRS>(p, g, ids, 0, row, kg, kr, vr);
 
     if (rope && p.rotate_query) {
         // Rotate-half of the query in place: the partner of chunk kb is
@@ -231,9 +242,10 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
             sm_new_v[lane + 64] = nv_hi;
             if (blk >= 0) {
                 const size_t slab = (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems;
-                // key (append_row, d) at (d/8)*128 + append_row*8 + d%8; value at d*16 + append_row
-                p.key_cache[slab + (lane >> 3) * 128 + append_row * 8 + (lane & 7)] = k_lo;
-                p.key_cache[slab + ((lane + 64) >> 3) * 128 + append_row * 8 + (lane & 7)] = k_hi;
+                // key (append_row, d) at (d/8)*128 + key_slot(append_row)*8 + d%8; value at d*16 + append_row
+                const int kslot = key_slot(append_row);
+                p.key_cache[slab + (lane >> 3) * 128 + kslot * 8 + (lane & 7)] = k_lo;
+                p.key_cache[slab + ((lane + 64) >> 3) * 128 + kslot * 8 + (lane & 7)] = k_hi;
                 p.value_cache[slab + lane * 16 + append_row] = nv_lo;
                 p.value_cache[slab + (lane + 64) * 16 + append_row] = nv_hi;
             }
@@ -248,35 +260,46 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
     for (int c = 0; c < 8; ++c) o[c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     for (int chunk = 0; ws < part_end; ++chunk, ws += WAVES * kChunkTokens) {
-        if (chunk > 0) load_chunk(p, g, ids, chunk, row, kg, kr, vr);
+        if (chunk > 0) load_chunk<PAIRS>(p, g, ids, chunk, row, kg, kr, vr);
 
-        // Patch the appended row of the keys (the tile loads may predate the
-        // append).
+        // Patch the appended key (the tile loads may predate the append): its
+        // slot is row (ti & 1)*8 + (slot & 7) of score MFMA slot >> 3 of pair
+        // ti >> 1.
         const int ti = append_tile - (ws >> 4);  // chunk tile holding the appended row
-        if (ti >= 0 && ti < TILES && row == append_row) {
+        if (ti >= 0 && ti < kChunkTiles) {
+            const int slot = key_slot(append_row);
+            if (row == (ti & 1) * 8 + (slot & 7)) {
 #pragma unroll
-            for (int i = 0; i < TILES; ++i) {
-                if (i != ti) continue;
+                for (int j = 0; j < PAIRS; ++j)
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-                    kr[i][kb] = *reinterpret_cast<const half8_t *>(sm_new_k + (kb * 4 + kg) * 8);
+                    for (int h = 0; h < 2; ++h) {
+                        if (j != (ti >> 1) || h != (slot >> 3)) continue;
+#pragma unroll
+                        for (int kb = 0; kb < 4; ++kb)
+                            kr[j][h][kb] = *reinterpret_cast<const half8_t *>(sm_new_k + (kb * 4 + kg) * 8);
+                    }
             }
         }
 
-        // Scores: lane holds tokens ws + i*16 + kg*4 + r (r = 0..3) of head `row`.
-        float x[TILES][4];
+        // Scores: MFMA h of pair j leaves lane (head `row`, kg) the tokens
+        // (kg & 1)*8 + h*4 + r (r = 0..3) of the pair's tile kg >> 1, so
+        // x[j][0..7] are 8 consecutive tokens of one tile.
+        float x[PAIRS][8];
         float cmax = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < TILES; ++i) {
-            float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < PAIRS; ++j) {
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[i][kb], qb[kb], acc, 0, 0, 0);
-            const int tbase = ws + i * 16 + kg * 4;
+            for (int h = 0; h < 2; ++h) {
+                float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                x[i][r] = (tbase + r < part_end) ? acc[r] * p.scale_log2 : -INFINITY;
-                cmax = fmaxf(cmax, x[i][r]);
+                for (int kb = 0; kb < 4; ++kb)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[j][h][kb], qb[kb], acc, 0, 0, 0);
+                const int tbase = ws + (2 * j + (kg >> 1)) * 16 + (kg & 1) * 8 + h * 4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    x[j][h * 4 + r] = (tbase + r < part_end) ? acc[r] * p.scale_log2 : -INFINITY;
+                    cmax = fmaxf(cmax, x[j][h * 4 + r]);
+                }
             }
         }
         cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
@@ -296,45 +319,41 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
             }
         }
 
-        // Values: zero the tiles past the partition and the rows after the
-        // appended one (their weights are 0, but they may hold poison and
-        // NaN * 0 would reach P.V); patch the appended row.
+        // Values: lane (dim, kg) holds tokens (kg & 1)*8 + e of tile
+        // 2j + (kg >> 1).  Zero the tiles past the partition and the tokens
+        // after the appended one (their weights are 0, but they may hold
+        // poison and NaN * 0 would reach P.V); patch the appended token.
+        if (ws + kChunkTokens > part_end || (ti >= 0 && ti < kChunkTiles)) {  // uniform
 #pragma unroll
-        for (int i = 0; i < TILES; ++i) {
-            if (ws + i * 16 >= part_end) {
+        for (int j = 0; j < PAIRS; ++j) {
+            const int tile = 2 * j + (kg >> 1);
+            const bool past = ws + tile * 16 >= part_end;
+            const bool append_here = tile == ti;
 #pragma unroll
-                for (int c = 0; c < 8; ++c) vr[i][c] = half4_t{};
-            }
-        }
-        if (ti >= 0 && ti < TILES) {
+            for (int e = 0; e < 8; ++e) {
+                const int tok = (kg & 1) * 8 + e;
+                const bool zero = past || (append_here && tok > append_row);
+                const bool patch = append_here && tok == append_row;
 #pragma unroll
-            for (int i = 0; i < TILES; ++i) {
-                if (i != ti) continue;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int r = kg * 4 + j;
-#pragma unroll
-                    for (int c = 0; c < 8; ++c) {
-                        if (r == append_row)
-                            vr[i][c][j] = __builtin_bit_cast(_Float16, sm_new_v[c * 16 + row]);
-                        else if (r > append_row)
-                            vr[i][c][j] = static_cast<_Float16>(0.0f);
-                    }
+                for (int c = 0; c < 8; ++c) {
+                    const _Float16 v = patch ? __builtin_bit_cast(_Float16, sm_new_v[c * 16 + row]) : vr[j][c][e];
+                    vr[j][c][e] = zero ? static_cast<_Float16>(0.0f) : v;
                 }
             }
         }
+        }
 
 #pragma unroll
-        for (int i = 0; i < TILES; ++i) {
-            half4_t pa;
+        for (int j = 0; j < PAIRS; ++j) {
+            half8_t pa;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const _Float16 ph = to_h(__builtin_amdgcn_exp2f(x[i][r] - m_new));
-                pa[r] = ph;
+            for (int e = 0; e < 8; ++e) {
+                const _Float16 ph = to_h(__builtin_amdgcn_exp2f(x[j][e] - m_new));
+                pa[e] = ph;
                 l_run += static_cast<float>(ph);  // the weights P.V actually uses
             }
 #pragma unroll
-            for (int c = 0; c < 8; ++c) o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vr[i][c], o[c], 0, 0, 0);
+            for (int c = 0; c < 8; ++c) o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vr[j][c], o[c], 0, 0, 0);
         }
     }
     l_run += __shfl_xor(l_run, 16);
@@ -362,9 +381,13 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
     }
     __syncthreads();
 
-    // Each thread owns kPer consecutive output elements of one head.
-    constexpr int kPer = (kGroup * kHeadDim) / kThreads;
-    const int e0 = threadIdx.x * kPer;
+    // Each of the first kCT threads (a power of two) owns kPer consecutive
+    // output elements of one head; the others shadow thread 0 and store
+    // nothing.
+    constexpr int kCT = kThreads >= 1024 ? 1024 : (kThreads >= 512 ? 512 : (kThreads >= 256 ? 256 : 128));
+    constexpr int kPer = (kGroup * kHeadDim) / kCT;
+    const bool active = threadIdx.x < kCT;
+    const int e0 = active ? static_cast<int>(threadIdx.x) * kPer : 0;
     const int h = e0 >> 7, d0 = e0 & 127;
     float M = -INFINITY;
 #pragma unroll
@@ -384,8 +407,10 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
     uint16_t *out = p.out + (static_cast<size_t>(s) * kQueryHeads + g * kGroup) * kHeadDim;
     if (num_parts == 1) {
         const float inv = 1.0f / L;
+        if (active) {
 #pragma unroll
-        for (int e = 0; e < kPer; ++e) out[e0 + e] = __builtin_bit_cast(uint16_t, to_h(po[e] * inv));
+            for (int e = 0; e < kPer; ++e) out[e0 + e] = __builtin_bit_cast(uint16_t, to_h(po[e] * inv));
+        }
         return;
     }
 
@@ -394,11 +419,13 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
     float *part_ml = p.part_ml + (unit + part) * (2 * kGroup);  // [head][max, sum]
     if constexpr (DEFER_MERGE) {
         // The kernel boundary orders these stores before the merge kernel.
+        if (active) {
 #pragma unroll
-        for (int e = 0; e < kPer; ++e) part_o[e0 + e] = po[e];
-        if (d0 == 0) {
-            part_ml[2 * h] = M;
-            part_ml[2 * h + 1] = L;
+            for (int e = 0; e < kPer; ++e) part_o[e0 + e] = po[e];
+            if (d0 == 0) {
+                part_ml[2 * h] = M;
+                part_ml[2 * h + 1] = L;
+            }
         }
         return;
     }
@@ -410,12 +437,14 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
     // 0 counts the arrival, which orders the partials before the count.
     // (A C++ release/acquire fence at agent scope would instead write back and
     // invalidate the whole L2 of the XCD in every workgroup.)
+    if (active) {
 #pragma unroll
-    for (int e = 0; e < kPer; ++e)
-        __hip_atomic_store(part_o + e0 + e, po[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (d0 == 0) {
-        __hip_atomic_store(part_ml + 2 * h, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(part_ml + 2 * h + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int e = 0; e < kPer; ++e)
+            __hip_atomic_store(part_o + e0 + e, po[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d0 == 0) {
+            __hip_atomic_store(part_ml + 2 * h, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(part_ml + 2 * h + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     // Wait for this wave's partial stores to complete (a single-wave
     // workgroup's __syncthreads() emits no wait), then for every wave.
@@ -467,8 +496,10 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
         Mg = Mb;
     }
     const float inv = 1.0f / Lg;
+    if (active) {
 #pragma unroll
-    for (int e = 0; e < kPer; ++e) out[e0 + e] = __builtin_bit_cast(uint16_t, to_h(og[e] * inv));
+        for (int e = 0; e < kPer; ++e) out[e0 + e] = __builtin_bit_cast(uint16_t, to_h(og[e] * inv));
+    }
     if (threadIdx.x == 0)
         __hip_atomic_store(p.counters + s * kKvHeads + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -483,7 +514,7 @@ __device__ inline int64_t checked_cache_len(const DecodeParams &p, int64_t len) 
 
 // Grid (partition, kv head, sequence): sequences of one uniform length, or
 // ragged lengths when there are too many sequences for the ragged kernel.
-template <int WAVES, int TILES>
+template <int WAVES, int PAIRS>
 __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParams p) {
     const uint32_t part = blockIdx.x;
     const uint32_t g = blockIdx.y;  // kv head
@@ -500,9 +531,10 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     if (part_start > cache_len) return;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     bool bad = false;
-    const uint32_t ids = wave_tile_ids<WAVES, TILES>(p, s, part_start, min(part_start + P, cache_len + 1), wave, &bad);
+    const uint32_t ids =
+        wave_tile_ids<WAVES, 2 * PAIRS>(p, s, part_start, min(part_start + P, cache_len + 1), wave, &bad);
     const int pos = p.positions ? load_const(p.positions, s) : cache_len;
-    decode_item<WAVES, TILES, false>(p, s, g, part, cache_len, pos, ids, bad);
+    decode_item<WAVES, PAIRS, false>(p, s, g, part, cache_len, pos, ids, bad);
 }
 
 // Exclusive scan of one int per thread over the workgroup; *total receives
@@ -536,7 +568,7 @@ __device__ inline int workgroup_exclusive_scan(int v, int *sm_wave_sums, int *to
 // blockIdx.x + gridDim.x, ...  Sequences with fewer partitions launch no
 // empty workgroups, so every compute unit stays on real work, and the block
 // ids of the next item are loaded while the current one runs.
-template <int WAVES, int TILES>
+template <int WAVES, int PAIRS>
 __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(DecodeParams p, uint32_t num_seqs) {
     constexpr int kThreads = WAVES * 64;
     __shared__ int sm_first[kMaxRaggedSeqs + 1];  // first item (per kv head) of each sequence
@@ -586,7 +618,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
     uint32_t s = 0, part = 0;
     locate(item >> 1, &s, &part);
     bool bad = false;
-    uint32_t ids = wave_tile_ids<WAVES, TILES>(p, s, static_cast<int>(part) * P,
+    uint32_t ids = wave_tile_ids<WAVES, 2 * PAIRS>(p, s, static_cast<int>(part) * P,
                                                min(static_cast<int>(part + 1) * P, sm_len[s] + 1), wave, &bad);
     for (;;) {
         const int next = item + static_cast<int>(gridDim.x);
@@ -594,11 +626,11 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
         bool bad_next = false;
         if (next < items) {
             locate(next >> 1, &s_next, &part_next);
-            ids_next = wave_tile_ids<WAVES, TILES>(p, s_next, static_cast<int>(part_next) * P,
+            ids_next = wave_tile_ids<WAVES, 2 * PAIRS>(p, s_next, static_cast<int>(part_next) * P,
                                                    min(static_cast<int>(part_next + 1) * P, sm_len[s_next] + 1), wave,
                                                    &bad_next);
         }
-        decode_item<WAVES, TILES, true>(p, s, static_cast<uint32_t>(item & 1), part, sm_len[s], sm_pos[s], ids, bad);
+        decode_item<WAVES, PAIRS, true>(p, s, static_cast<uint32_t>(item & 1), part, sm_len[s], sm_pos[s], ids, bad);
         if (next >= items) break;
         __syncthreads();  // the next item reuses the workgroup's LDS
         item = next;
@@ -734,53 +766,38 @@ int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
     p.scale_log2 = kLog2e / sqrtf(static_cast<float>(kHeadDim));
 
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const uint32_t part_tiles = (launch.partition_tokens + kBlockTokens - 1) / kBlockTokens;
     int e = 0;
-    // Streaming regime (ragged lengths, or partitions longer than one chunk
-    // of 8 waves): the persistent kernel stores partials and a second kernel
-    // merges them, so no workgroup waits on a cross-workgroup hand-off.  Its
-    // workgroups are 4 waves of 2 tiles (several resident per compute unit).
-    const bool streaming = (a.cache_lens != nullptr || part_tiles > kSingleShotTiles) && a.num_seqs <= kMaxRaggedSeqs;
-    if (streaming) {
+    if (launch.streaming) {
+        // Persistent kernel storing partials, then the merge kernel: no
+        // workgroup waits on a cross-workgroup hand-off.
         const uint64_t max_items = static_cast<uint64_t>(launch.max_parts) * kKvHeads * a.num_seqs;
-#define PVLC_RAGGED_LAUNCH(W, TL)                                                                                  \
+#define PVLC_RAGGED_LAUNCH(W, PR)                                                                                  \
     do {                                                                                                           \
-        const uint32_t wgs = resident_workgroups(reinterpret_cast<const void *>(&paged_decode_ragged_kernel<W, TL>), \
+        const uint32_t wgs = resident_workgroups(reinterpret_cast<const void *>(&paged_decode_ragged_kernel<W, PR>), \
                                                  (W) * 64, max_items, &e);                                         \
         if (e == 0) {                                                                                              \
-            hipLaunchKernelGGL((paged_decode_ragged_kernel<W, TL>), dim3(wgs), dim3((W) * 64), 0, st, p, a.num_seqs); \
+            hipLaunchKernelGGL((paged_decode_ragged_kernel<W, PR>), dim3(wgs), dim3((W) * 64), 0, st, p, a.num_seqs); \
             hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(kKvHeads, a.num_seqs), dim3(256), 0, st, p);       \
         }                                                                                                          \
     } while (0)
-        if (part_tiles >= 8) PVLC_RAGGED_LAUNCH(4, 2);
-        else if (part_tiles >= 4) PVLC_RAGGED_LAUNCH(4, 1);
+        if (launch.waves == 4) PVLC_RAGGED_LAUNCH(4, 1);
         else PVLC_RAGGED_LAUNCH(2, 1);
 #undef PVLC_RAGGED_LAUNCH
         if (e != 0) return e;
         return static_cast<int>(hipGetLastError());
     }
 
-    // Single-shot regime: one workgroup per (partition, kv head, sequence),
-    // TILES blocks of 16 tokens per wave and the fewest of 2, 4 or 8 waves
-    // that cover the partition; the last partition to finish merges.
-    const uint32_t tiles = launch.tiles_per_wave;
-    const uint32_t need = (part_tiles + tiles - 1) / tiles;
-    const uint32_t waves = need <= 2 ? 2 : (need <= 4 ? 4 : 8);
+    // Single-shot regime: one workgroup per (partition, kv head, sequence);
+    // the last partition to finish merges.
     const dim3 grid(launch.max_parts, kKvHeads, a.num_seqs);
-#define PVLC_DECODE_LAUNCH(W, TL) hipLaunchKernelGGL((paged_decode_kernel<W, TL>), grid, dim3((W) * 64), 0, st, p)
-#define PVLC_DECODE_WAVES(TL)                                   \
-    do {                                                        \
-        if (waves == 2) PVLC_DECODE_LAUNCH(2, TL);              \
-        else if (waves == 4) PVLC_DECODE_LAUNCH(4, TL);         \
-        else PVLC_DECODE_LAUNCH(8, TL);                         \
-    } while (0)
-    switch (tiles) {
-        case 1: PVLC_DECODE_WAVES(1); break;
-        case 2: PVLC_DECODE_WAVES(2); break;
-        case 3: PVLC_DECODE_WAVES(3); break;
-        default: PVLC_DECODE_WAVES(4); break;
+#define PVLC_DECODE_LAUNCH(W, PR) hipLaunchKernelGGL((paged_decode_kernel<W, PR>), grid, dim3((W) * 64), 0, st, p)
+    switch (launch.waves) {
+        case 2: PVLC_DECODE_LAUNCH(2, 1); break;
+        case 4: PVLC_DECODE_LAUNCH(4, 1); break;
+        case 6: PVLC_DECODE_LAUNCH(6, 1); break;
+        case 12: PVLC_DECODE_LAUNCH(12, 1); break;
+        default: PVLC_DECODE_LAUNCH(8, 1); break;
     }
-#undef PVLC_DECODE_WAVES
 #undef PVLC_DECODE_LAUNCH
     return static_cast<int>(hipGetLastError());
 }

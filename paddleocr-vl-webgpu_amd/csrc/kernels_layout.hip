@@ -32,7 +32,7 @@ __global__ void kv_pack_kernel(const uint16_t *__restrict__ key_rows, const uint
     const uint32_t tt = t % kBlockTokens;
     const size_t src = (static_cast<size_t>(t) * kKvHeads + h) * kHeadDim + chunk * 8;
     const u16x8_t k = *reinterpret_cast<const u16x8_t *>(key_rows + src);
-    *reinterpret_cast<u16x8_t *>(key_cache + slab + chunk * 128 + tt * 8) = k;
+    *reinterpret_cast<u16x8_t *>(key_cache + slab + chunk * 128 + key_slot(tt) * 8) = k;
     const u16x8_t v = *reinterpret_cast<const u16x8_t *>(value_rows + src);
 #pragma unroll
     for (int j = 0; j < 8; ++j) value_cache[slab + (chunk * 8 + j) * kBlockTokens + tt] = v[j];
@@ -56,7 +56,7 @@ __global__ void kv_unpack_kernel(const uint16_t *__restrict__ key_cache, const u
     const size_t slab = (static_cast<size_t>(b) * kKvHeads + h) * kBlockHeadElems;
     const uint32_t tt = t % kBlockTokens;
     *reinterpret_cast<u16x8_t *>(key_rows + dst) =
-        *reinterpret_cast<const u16x8_t *>(key_cache + slab + chunk * 128 + tt * 8);
+        *reinterpret_cast<const u16x8_t *>(key_cache + slab + chunk * 128 + key_slot(tt) * 8);
     u16x8_t v;
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = value_cache[slab + (chunk * 8 + j) * kBlockTokens + tt];

@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void prefill_rope_append_kernel(PrefillParams 
             const uint16_t *krow = p.key + (static_cast<size_t>(t) * kKvHeads + hh) * kHeadDim;
             const half8_t k = rope ? rotate_chunk(krow, d0, cos_row, sin_row)
                                    : *reinterpret_cast<const half8_t *>(krow + d0);
-            *reinterpret_cast<half8_t *>(p.key_cache + slab + c * 128 + tt * 8) = k;
+            *reinterpret_cast<half8_t *>(p.key_cache + slab + c * 128 + key_slot(tt) * 8) = k;
         } else {
             const u16x8_t v = *reinterpret_cast<const u16x8_t *>(p.value + (static_cast<size_t>(t) * kKvHeads + hh) *
                                                                                     kHeadDim + d0);
@@ -173,7 +173,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
         for (int i = 0; i < kStepTiles; ++i) {
             half8_t kf[4];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) kf[kb] = *reinterpret_cast<const half8_t *>(&sk[i][(kb * 4 + kg) * 128 + row * 8]);
+            for (int kb = 0; kb < 4; ++kb)
+                kf[kb] = *reinterpret_cast<const half8_t *>(&sk[i][(kb * 4 + kg) * 128 + key_slot(row) * 8]);
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
                 float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};

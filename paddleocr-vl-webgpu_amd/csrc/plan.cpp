@@ -296,7 +296,8 @@ bool fp16_representable(const float *values, size_t n) {
 
 size_t key_blocked_index(uint32_t token, uint32_t head, uint32_t dim) {
     const size_t block = token / kBlockTokens, t = token % kBlockTokens;
-    return ((block * kKvHeads + head) * (kHeadDim / 8) + dim / 8) * (kBlockTokens * 8) + t * 8 + dim % 8;
+    return ((block * kKvHeads + head) * (kHeadDim / 8) + dim / 8) * (kBlockTokens * 8) +
+           static_cast<size_t>(key_slot(static_cast<int>(t))) * 8 + dim % 8;
 }
 
 size_t value_blocked_index(uint32_t token, uint32_t head, uint32_t dim) {
@@ -317,13 +318,18 @@ DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts) {
     return w;
 }
 
-uint32_t auto_tiles_per_wave(uint32_t partition_tokens) {
-    // Single-shot partitions (at most 8 waves x 4 tiles) give each wave the
-    // fewest tiles that cover the partition with 8 waves; longer partitions
-    // loop over 8 waves x 4 tiles.
+DecodeShape decode_shape(uint32_t partition_tokens, bool streaming) {
     const uint32_t tiles = (partition_tokens + kBlockTokens - 1) / kBlockTokens;
-    if (tiles > kSingleShotTiles) return 4;
-    return (tiles + 7) / 8;
+    if (streaming) return tiles >= 8 ? DecodeShape{4, 1} : DecodeShape{2, 1};
+    // Single shot: the smallest workgroup of 2, 4, 6, 8 or 12 waves holding
+    // one pair of tiles each that covers the partition; longer partitions
+    // loop over 8 waves.
+    if (tiles <= 4) return {2, 1};
+    if (tiles <= 8) return {4, 1};
+    if (tiles <= 12) return {6, 1};
+    if (tiles <= 16) return {8, 1};
+    if (tiles <= 24) return {12, 1};
+    return {8, 1};
 }
 
 uint32_t balanced_parts(uint32_t num_seqs) {
@@ -336,16 +342,17 @@ uint32_t single_shot_partition(uint32_t num_seqs, uint32_t context) {
     // Split every (sequence, kv head) into the same number of partitions so
     // that about one workgroup per compute unit covers the whole step in one
     // round, each partition a whole number of 16-token tiles.
-    // Partitions are rounded up to whole waves (1, 2, 4 or a multiple of 8
-    // tiles, so no wave of a full partition idles); the last partition of
-    // each sequence is then the short one.
+    // Partitions are rounded up to the tile capacity of a single-shot shape
+    // (decode_shape), so no wave of a full partition idles; the last
+    // partition of each sequence is then the short one.
     const uint32_t tiles = (context + kBlockTokens - 1) / kBlockTokens;
     const uint32_t parts = balanced_parts(num_seqs);
     uint32_t part_tiles = (tiles + parts - 1) / parts;
-    if (part_tiles > 8) part_tiles = (part_tiles + 7) / 8 * 8;
-    else if (part_tiles > 4) part_tiles = 8;
-    else if (part_tiles == 3) part_tiles = 4;
-    return part_tiles <= kSingleShotTiles ? part_tiles * kBlockTokens : 0;
+    static const uint32_t kCapacities[] = {4, 8, 12, 16, 24};  // tiles of the single-shot shapes
+    for (uint32_t c : kCapacities) {
+        if (part_tiles <= c) return c * kBlockTokens;
+    }
+    return 0;
 }
 
 uint32_t auto_partition(uint32_t num_seqs, uint32_t context) {

@@ -16,14 +16,25 @@ constexpr uint32_t kGroup = kQueryHeads / kKvHeads;
 constexpr uint32_t kBlockTokens = PVLC_HIP_BLOCK_TOKENS;
 constexpr uint32_t kRowElems = kKvHeads * kHeadDim;          // one cache row, both heads
 constexpr uint32_t kBlockHeadElems = kBlockTokens * kHeadDim;  // one (block, head) slab
+
+// Key slot of token t (0..15) inside a 16-token block of the key plane: bits
+// 2 and 3 of t swapped, so that slots 0-7 hold tokens 0-3 and 8-11 and slots
+// 8-15 tokens 4-7 and 12-15.  With this order one 16x16x32 score MFMA over
+// rows "slots 0-7 of tile A, slots 0-7 of tile B" (and a second over slots
+// 8-15) leaves each lane the scores of 8 consecutive tokens of one tile:
+// exactly the probability operand of a 16x16x32 P.V MFMA whose values are
+// 16-byte loads.  The map is its own inverse (constexpr: usable on host and
+// device).
+constexpr int key_slot(int t) { return (t & 3) | ((t & 4) << 1) | ((t & 8) >> 1); }
 constexpr uint32_t kMaxDecoderHeadDim = 128;                   // runtime-core lib.rs:180
 constexpr uint32_t kMaxWebgpuDispatch = 65535;                 // runtime-core lib.rs:187
 constexpr uint32_t kMaxMergeParts = 64;  // split-K partitions one in-kernel merge combines
 // Automatic partitioning: workgroups one launch aims to keep resident (one
 // per MI355X compute unit), the most tiles one workgroup covers without
-// looping (8 waves x 4 tiles), and the most partitions of the balanced rule.
+// looping (12 waves x one pair of tiles), and the most partitions of the
+// balanced rule.
 constexpr uint32_t kTargetWorkgroups = 256;
-constexpr uint32_t kSingleShotTiles = 32;
+constexpr uint32_t kSingleShotTiles = 24;
 constexpr uint32_t kMaxBalancedParts = 16;
 // Sequences the ragged (persistent) decode kernel numbers in LDS; launches
 // with more ragged sequences use one workgroup per (partition, head, sequence).
@@ -69,7 +80,9 @@ size_t value_blocked_index(uint32_t token, uint32_t head, uint32_t dim);
 struct DecodeLaunch {
     const pvlc_hip_paged_decode_args *args;
     uint32_t partition_tokens;
-    uint32_t tiles_per_wave;  // 16-token blocks a wave holds per chunk: 1..4
+    uint32_t waves;      // waves per workgroup
+    uint32_t pairs;      // pairs of 16-token tiles a wave holds per chunk
+    bool streaming;      // persistent kernel + merge kernel (else one workgroup per partition)
     uint32_t max_parts;
     float *part_o;
     float *part_ml;
@@ -99,6 +112,11 @@ uint32_t balanced_parts(uint32_t num_seqs);
 uint32_t single_shot_partition(uint32_t num_seqs, uint32_t context);
 uint32_t auto_partition(uint32_t num_seqs, uint32_t context);
 uint32_t auto_workspace_parts(uint32_t num_seqs, uint32_t max_context);
-uint32_t auto_tiles_per_wave(uint32_t partition_tokens);
+// Launch shape for a partition: (waves, pairs) of the single-shot kernel,
+// or of the persistent kernel when `streaming`.
+struct DecodeShape {
+    uint32_t waves, pairs;
+};
+DecodeShape decode_shape(uint32_t partition_tokens, bool streaming);
 
 }  // namespace pvlc

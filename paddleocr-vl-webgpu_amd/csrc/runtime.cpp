@@ -142,9 +142,16 @@ pvlc_hip_status launch_decode_checked(const pvlc_hip_paged_decode_args *a, void 
     DecodeWorkspace layout{};
     if (pvlc_hip_status st = validate_decode_args(a, &partition, &max_parts, &layout)) return st;
     char *ws = static_cast<char *>(a->workspace);
+    // Streaming regime: ragged lengths, or partitions longer than one chunk
+    // of the largest single-shot workgroup.
+    const uint32_t part_tiles = (partition + kBlockTokens - 1) / kBlockTokens;
+    const bool streaming = (a->cache_lens != nullptr || part_tiles > kSingleShotTiles) && a->num_seqs <= kMaxRaggedSeqs;
+    const DecodeShape shape = decode_shape(partition, streaming);
     DecodeLaunch launch{a,
                         partition,
-                        auto_tiles_per_wave(partition),
+                        shape.waves,
+                        shape.pairs,
+                        streaming,
                         max_parts,
                         reinterpret_cast<float *>(ws + layout.part_o_offset),
                         reinterpret_cast<float *>(ws + layout.part_ml_offset),

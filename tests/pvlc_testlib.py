@@ -38,6 +38,12 @@ def check_close(actual, expected, label="", atol=ATOL, rel=REL_L2):
     return max_abs, rel_l2
 
 
+def key_slot(t):
+    """Slot of token t inside a 16-token block of the key plane: bits 2 and 3 swapped."""
+    t = np.asarray(t)
+    return (t & 3) | ((t & 4) << 1) | ((t & 8) >> 1)
+
+
 def scatter_rows(plane_k, plane_v, k_rows, v_rows, tokens, table):
     """Write rows 0..tokens-1 of one sequence into blocked planes through its block table."""
     t = np.arange(tokens)
@@ -45,7 +51,7 @@ def scatter_rows(plane_k, plane_v, k_rows, v_rows, tokens, table):
     tt = t % 16
     for h in range(2):
         for d in range(128):
-            kidx = ((blk * 2 + h) * 16 + d // 8) * 128 + tt * 8 + d % 8
+            kidx = ((blk * 2 + h) * 16 + d // 8) * 128 + key_slot(tt) * 8 + d % 8
             vidx = ((blk * 2 + h) * 128 + d) * 16 + tt
             plane_k[kidx] = k_rows.reshape(tokens, 2, 128)[:, h, d]
             plane_v[vidx] = v_rows.reshape(tokens, 2, 128)[:, h, d]
@@ -59,7 +65,7 @@ def gather_rows(plane_k, plane_v, tokens, table):
     v = np.zeros((tokens, 2, 128), np.uint16)
     for h in range(2):
         for d in range(128):
-            k[:, h, d] = plane_k[((blk * 2 + h) * 16 + d // 8) * 128 + tt * 8 + d % 8]
+            k[:, h, d] = plane_k[((blk * 2 + h) * 16 + d // 8) * 128 + key_slot(tt) * 8 + d % 8]
             v[:, h, d] = plane_v[((blk * 2 + h) * 128 + d) * 16 + tt]
     return k.ravel(), v.ravel()
 
