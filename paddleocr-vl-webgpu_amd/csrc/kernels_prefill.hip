@@ -9,13 +9,19 @@
 //
 // Kernel 2: one workgroup per (16-token query block, kv head) serves the 8
 // query heads of the group; each of its 4 waves owns 2 heads, i.e. two
-// 16-column MFMA tiles of query rows.  Keys and values stream through LDS in
-// steps of 64 keys (4 cache blocks), straight in MFMA operand order, with the
-// next step prefetched into registers while the current one is computed:
-//   S^T[key][row] = K . Q^T          v_mfma_f32_16x16x32_f16
-//   O[row][dim]  += P[row][key] V     v_mfma_f32_16x16x16_f16
-// with an online softmax in log2 units and the causal mask on the diagonal
-// steps.  Query blocks are scheduled latest (heaviest) first.  Replaces
+// 16-column MFMA tiles of query rows.  Keys and values stream through
+// double-buffered LDS in steps of 64 keys (2 pairs of cache blocks), laid out
+// so every operand read is conflict-free, with the next step loaded into
+// registers while the current one is computed:
+//   S^T[key][row] = K . Q^T           v_mfma_f32_16x16x32_f16
+//   O[row][dim]  += P[row][key] V      v_mfma_f32_16x16x32_f16
+//   l[row]       += P[row][key] 1      (same MFMA, ones operand)
+// The key slot order of the cache (key_slot) makes the score MFMA leave each
+// lane 8 consecutive keys of one tile, which is the P operand of the P.V MFMA.
+// Online softmax in log2 units (scale folded into one FMA per score), the
+// causal mask only on steps that reach the diagonal, and the rescale skipped
+// while the running max is unchanged.  Heavy and light query blocks are
+// paired over the grid for balance.  Replaces
 // decoder_prefill_gqa_f32 (crates/pvlc-wgsl/src/lib.rs:1262-1332); arithmetic
 // reference causal_gqa_f32 (crates/pvlc-cpu-ref/src/lib.rs:782-853).
 
@@ -106,11 +112,39 @@ __global__ __launch_bounds__(256) void prefill_rope_append_kernel(PrefillParams 
     }
 }
 
+// LDS layouts of one 64-key step (2 pairs of 16-token tiles), chosen so every
+// 16-lane group of an MFMA operand read is one contiguous 256-byte run (no
+// bank conflicts):
+//   keys   [pair][16 dim-chunks][score MFMA h][tile of pair][8 slots][8 dims]
+//   values [pair][tile of pair][token half][128 dims][8 tokens]
+constexpr int kStepElems = kStepTiles * kBlockHeadElems;  // fp16 elements per plane and step
+
+__device__ inline int lds_key_offset(int j, int chunk, int h, int tile, int slot8) {
+    return ((((j * 16 + chunk) * 2 + h) * 2 + tile) * 8 + slot8) * 8;
+}
+__device__ inline int lds_value_offset(int j, int tile, int half, int dim) {
+    return (((j * 2 + tile) * 2 + half) * kHeadDim + dim) * 8;
+}
+
+// Work item b of the grid: query blocks are paired heaviest with lightest,
+// so that the two items a compute unit runs (b and b + qblocks, dispatched
+// in order) sum to about the same number of key steps everywhere.
+__device__ inline void prefill_item(int b, int qblocks, int *qb, uint32_t *g) {
+    if (b < qblocks) {
+        *qb = qblocks - 1 - b;
+        *g = 0;
+    } else {
+        *qb = b - qblocks;
+        *g = 1;
+    }
+}
+
 __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(PrefillParams p) {
     const int n = static_cast<int>(p.tokens);
     const int qblocks = (n + kQueryBlock - 1) / kQueryBlock;
-    const int qb = qblocks - 1 - static_cast<int>(blockIdx.x);  // heaviest first
-    const uint32_t g = blockIdx.y;
+    int qb;
+    uint32_t g;
+    prefill_item(static_cast<int>(blockIdx.x), qblocks, &qb, &g);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int row = lane & 15, kg = lane >> 4;
@@ -134,113 +168,154 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     const int steps = (nkeys + kKeyStep - 1) / kKeyStep;
     const int last_tile = (nkeys - 1) >> 4;
 
-    __shared__ uint16_t sk[kStepTiles][kBlockHeadElems];
-    __shared__ uint16_t sv[kStepTiles][kBlockHeadElems];
-    u16x8_t pk[kStepTiles], pv[kStepTiles];
+    // Double-buffered LDS; each thread moves 4 key and 4 value chunks of 16
+    // bytes per step through registers (loaded one step ahead).
+    __shared__ uint16_t sk[2][kStepElems];
+    __shared__ uint16_t sv[2][kStepElems];
+    u16x8_t pk[4], pv[4];
+    int koff[4], voff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = static_cast<int>(threadIdx.x) + i * (kWaves * 64);  // chunk 0..1023 of the step
+        // keys: c = tile*256 + chunk*16 + slot
+        const int kt = c >> 8, kchunk = (c >> 4) & 15, kslot = c & 15;
+        koff[i] = lds_key_offset(kt >> 1, kchunk, kslot >> 3, kt & 1, kslot & 7);
+        // values: c = tile*256 + dim*2 + half
+        const int vt = c >> 8, vdim = (c >> 1) & 127, vhalf = c & 1;
+        voff[i] = lds_value_offset(vt >> 1, vt & 1, vhalf, vdim);
+    }
     auto gload = [&](int step) {
 #pragma unroll
-        for (int i = 0; i < kStepTiles; ++i) {
+        for (int i = 0; i < 4; ++i) {
+            const int c = static_cast<int>(threadIdx.x) + i * (kWaves * 64);
             bool ok;
-            const uint32_t blk = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + i, last_tile)), &ok);
+            const uint32_t blk = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + (c >> 8), last_tile)), &ok);
             const size_t slab = (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems;
-            pk[i] = *reinterpret_cast<const u16x8_t *>(p.key_cache + slab + threadIdx.x * 8);
-            pv[i] = *reinterpret_cast<const u16x8_t *>(p.value_cache + slab + threadIdx.x * 8);
+            pk[i] = *reinterpret_cast<const u16x8_t *>(p.key_cache + slab + (c & 255) * 8);
+            pv[i] = *reinterpret_cast<const u16x8_t *>(p.value_cache + slab + (c & 255) * 8);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *reinterpret_cast<u16x8_t *>(&sk[buf][koff[i]]) = pk[i];
+            *reinterpret_cast<u16x8_t *>(&sv[buf][voff[i]]) = pv[i];
         }
     };
 
-    float m_run[2] = {-INFINITY, -INFINITY};
-    float l_run[2] = {0.f, 0.f};
-    float4_t o[2][8];
+    float m_run[2] = {-INFINITY, -INFINITY};  // raw (unscaled) running max of this lane's column
+    float4_t o[2][9];                          // 8 column tiles of the output, then the row sums
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) o[ct][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < 9; ++c) o[ct][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+    half8_t ones;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ones[e] = static_cast<_Float16>(1.0f);
+    const float scale = p.scale_log2;
 
     gload(0);
+    lstore(0);
+    if (steps > 1) gload(1);
+    __syncthreads();
     for (int step = 0; step < steps; ++step) {
-        __syncthreads();  // every wave is done with the previous step's tiles
-#pragma unroll
-        for (int i = 0; i < kStepTiles; ++i) {
-            *reinterpret_cast<u16x8_t *>(&sk[i][threadIdx.x * 8]) = pk[i];
-            *reinterpret_cast<u16x8_t *>(&sv[i][threadIdx.x * 8]) = pv[i];
-        }
-        __syncthreads();
-        if (step + 1 < steps) gload(step + 1);
-
+        const int buf = step & 1;
+        const uint16_t *kl = sk[buf];
+        const uint16_t *vl = sv[buf];
         const int kbase = step * kKeyStep;
-        float x[2][kStepTiles][4];
+        // Scores: MFMA h of pair j leaves lane (column = query token, kg) the
+        // keys (kg & 1)*8 + h*4 + r of the pair's tile kg >> 1.
+        float x[2][2][8];
 #pragma unroll
-        for (int i = 0; i < kStepTiles; ++i) {
-            half8_t kf[4];
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-                kf[kb] = *reinterpret_cast<const half8_t *>(&sk[i][(kb * 4 + kg) * 128 + key_slot(row) * 8]);
+            for (int h = 0; h < 2; ++h) {
+                float4_t acc[2] = {float4_t{0.f, 0.f, 0.f, 0.f}, float4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+                for (int kb = 0; kb < 4; ++kb) {
+                    const half8_t kf = *reinterpret_cast<const half8_t *>(
+                        kl + lds_key_offset(j, kb * 4 + kg, h, row >> 3, row & 7));
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kb], qf[ct][kb], acc, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int key = kbase + i * 16 + kg * 4 + r;
-                    x[ct][i][r] = (key <= my_token && key < n) ? acc[r] * p.scale_log2 : -INFINITY;
+                    for (int ct = 0; ct < 2; ++ct)
+                        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ct][kb], acc[ct], 0, 0, 0);
                 }
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) x[ct][j][h * 4 + r] = acc[ct][r];
             }
+        // The causal mask and the end of the sequence only touch steps that
+        // reach past the first query token of the block.
+        if (kbase + kKeyStep - 1 > t0 || kbase + kKeyStep > n) {  // uniform
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int key = kbase + (2 * j + (kg >> 1)) * 16 + (kg & 1) * 8 + e;
+                    const bool keep = key <= my_token && key < n;
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct) x[ct][j][e] = keep ? x[ct][j][e] : -INFINITY;
+                }
         }
-        half4_t pa[2][kStepTiles];
+        half8_t pa[2][2];
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
             float cmax = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < kStepTiles; ++i)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) cmax = fmaxf(cmax, x[ct][i][r]);
+                for (int e = 0; e < 8; ++e) cmax = fmaxf(cmax, x[ct][j][e]);
             cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
             cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
             // Step 0 always holds key 0 <= every query token, so m_new is finite.
             const float m_new = fmaxf(m_run[ct], cmax);
-            const float alpha = __builtin_amdgcn_exp2f(m_run[ct] - m_new);
-            l_run[ct] *= alpha;
-            m_run[ct] = m_new;
-            if (step > 0) {
+            const float ms = m_new * scale;
+            if (__any(m_new != m_run[ct]) && step > 0) {
+                const float alpha = __builtin_amdgcn_exp2f(m_run[ct] * scale - ms);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float a = __shfl(alpha, kg * 4 + r);
 #pragma unroll
-                    for (int c = 0; c < 8; ++c) o[ct][c][r] *= a;
+                    for (int c = 0; c < 9; ++c) o[ct][c][r] *= a;
                 }
             }
+            m_run[ct] = m_new;
 #pragma unroll
-            for (int i = 0; i < kStepTiles; ++i)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const _Float16 ph = to_h(__builtin_amdgcn_exp2f(x[ct][i][r] - m_new));
-                    pa[ct][i][r] = ph;
-                    l_run[ct] += static_cast<float>(ph);
-                }
+                for (int e = 0; e < 8; ++e)
+                    pa[ct][j][e] = to_h(__builtin_amdgcn_exp2f(__builtin_fmaf(x[ct][j][e], scale, -ms)));
         }
+        // P.V, and P.1 for the row sums (exactly the rounded weights P.V uses).
 #pragma unroll
-        for (int i = 0; i < kStepTiles; ++i)
+        for (int j = 0; j < 2; ++j) {
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const half4_t vf = *reinterpret_cast<const half4_t *>(&sv[i][(c * 16 + row) * 16 + kg * 4]);
+                const half8_t vf = *reinterpret_cast<const half8_t *>(
+                    vl + lds_value_offset(j, kg >> 1, kg & 1, c * 16 + row));
 #pragma unroll
                 for (int ct = 0; ct < 2; ++ct)
-                    o[ct][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[ct][i], vf, o[ct][c], 0, 0, 0);
+                    o[ct][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ct][j], vf, o[ct][c], 0, 0, 0);
             }
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+                o[ct][8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ct][j], ones, o[ct][8], 0, 0, 0);
+        }
+        if (step + 1 < steps) {
+            lstore(buf ^ 1);  // its last readers finished before the previous barrier
+            if (step + 2 < steps) gload(step + 2);
+        }
+        __syncthreads();
     }
 
     // Normalise: output row kg*4 + r of tile ct is query token t0 + kg*4 + r;
-    // its sum lives in the lanes whose column index is that row.
+    // its row sum is element r of the sums tile in the same lane.
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-        float l = l_run[ct];
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
         const int h = static_cast<int>(g) * kGroup + wave * 2 + ct;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float inv = 1.0f / __shfl(l, kg * 4 + r);
+            const float inv = 1.0f / o[ct][8][r];
             const int t = t0 + kg * 4 + r;
             if (t < n) {
                 uint16_t *orow = p.out + (static_cast<size_t>(t) * kQueryHeads + h) * kHeadDim;
@@ -276,7 +351,7 @@ int launch_prefill(const pvlc_hip_paged_prefill_args *a, void *stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     const unsigned qblocks = (a->tokens + kQueryBlock - 1) / kQueryBlock;
-    hipLaunchKernelGGL(prefill_attention_kernel, dim3(qblocks, kKvHeads), dim3(kWaves * 64), 0, st, p);
+    hipLaunchKernelGGL(prefill_attention_kernel, dim3(qblocks * kKvHeads), dim3(kWaves * 64), 0, st, p);
     return static_cast<int>(hipGetLastError());
 }
 
