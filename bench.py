@@ -342,13 +342,12 @@ def bench_prefill(args):
     kp = torch.empty(nb * 16 * W, dtype=torch.float16, device=dev)
     vp = torch.empty_like(kp)
     out = torch.empty(n * 2048, dtype=torch.float16, device=dev)
-    scratch = torch.empty(n * 2048, dtype=torch.float16, device=dev)
     cos, sin = pvlc.rope_table(ROPE_BASE, n)
     d_cos, d_sin = torch.from_numpy(cos.ravel()).to(dev), torch.from_numpy(sin.ravel()).to(dev)
 
     def call(i):
         pvlc.paged_prefill_f16(tokens=n, num_blocks=nb, key_cache=kp, value_cache=vp, query=q, key=k, value=v,
-                               out=out, query_scratch=scratch, rope_cos=d_cos, rope_sin=d_sin, rope_rows=n,
+                               out=out, rope_cos=d_cos, rope_sin=d_sin, rope_rows=n,
                                stream=stream)
 
     for i in range(args.warmup):

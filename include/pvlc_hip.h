@@ -364,7 +364,7 @@ typedef struct pvlc_hip_paged_prefill_args {
     const float *rope_sin;
     uint32_t rope_rows;
     const int32_t *positions; /* [N] or NULL = 0..N-1 */
-    uint16_t *query_scratch;  /* [N][16][128] fp16: the rotated query */
+    uint16_t *query_scratch;  /* optional [N][16][128] fp16: receives the rotated query (NULL: not written) */
     uint32_t *error_word;     /* optional: bit 1 = block id out of range (row skipped), bit 2 = position outside the rope table */
 } pvlc_hip_paged_prefill_args;
 

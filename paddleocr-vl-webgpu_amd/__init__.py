@@ -538,7 +538,7 @@ def paged_decode_f16(args: PagedDecodeArgsC, stream=None) -> None:
     _check(lib.pvlc_hip_paged_decode_f16(ctypes.byref(args), _stream(stream)))
 
 
-def paged_prefill_f16(*, tokens, num_blocks, key_cache, value_cache, query, key, value, out, query_scratch,
+def paged_prefill_f16(*, tokens, num_blocks, key_cache, value_cache, query, key, value, out, query_scratch=None,
                       block_table=None, rope_cos=None, rope_sin=None, rope_rows=0, positions=None,
                       error_word=None, stream=None) -> None:
     """Causal prefill with rotary and paged range append

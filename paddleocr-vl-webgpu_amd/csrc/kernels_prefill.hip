@@ -1,11 +1,12 @@
 // Causal prefill for gfx950: rotary + range append into the paged cache, then
 // MFMA flash attention over the cache.
 //
-// Kernel 1 (one workgroup per token): rotates the 16 query heads into a
-// scratch row, rotates the 2 key heads and writes them with the values into
-// the blocked cache (the same rounding as the decode append, so prefill and
-// decode leave bit-identical rows).  Replaces decoder_prefill_mrope_f32 and
-// decoder_kv_append_range_f32 (crates/pvlc-wgsl/src/lib.rs:1334-1416).
+// Kernel 1 (4 tokens per workgroup): rotates the 2 key heads and writes them
+// with the values into the blocked cache (the same rounding as the decode
+// append, so prefill and decode leave bit-identical rows), and, when the
+// caller passes a query scratch, writes the rotated queries there.  Replaces
+// decoder_prefill_mrope_f32 and decoder_kv_append_range_f32
+// (crates/pvlc-wgsl/src/lib.rs:1334-1416).
 //
 // Kernel 2: one workgroup per (16-token query block, kv head) serves the 8
 // query heads of the group; each of its 4 waves owns 2 heads, i.e. two
@@ -70,44 +71,61 @@ __device__ inline uint32_t cache_block(const PrefillParams &p, uint32_t tile, bo
     return *ok ? static_cast<uint32_t>(b) : 0u;
 }
 
+// Kernel 1: 4 tokens per workgroup, 64 threads per token: threads 0-31
+// rotate the token's 2 key heads (8 dims each) and write them into the
+// cache, threads 32-63 scatter its values.  With a query scratch the
+// workgroup also writes the rotated queries of its tokens (the attention
+// kernel rotates its own query fragments, so the scratch is only an output
+// for callers that want it).
+constexpr int kAppendTokens = 4;
+
 __global__ __launch_bounds__(256) void prefill_rope_append_kernel(PrefillParams p) {
-    const uint32_t t = blockIdx.x;
     const int i = threadIdx.x;
-    bool rope = p.rope_cos != nullptr;
-    const int pos = p.positions ? load_const(p.positions, t) : static_cast<int>(t);
-    if (rope && (pos < 0 || static_cast<uint32_t>(pos) >= p.rope_rows)) {
-        if (i == 0 && p.error_word) atomicOr(p.error_word, 4u);
-        rope = false;
-    }
-    const float *cos_row = rope ? p.rope_cos + static_cast<size_t>(pos) * 64 : nullptr;
-    const float *sin_row = rope ? p.rope_sin + static_cast<size_t>(pos) * 64 : nullptr;
-    // Query: thread = (head, 8-dim chunk).
-    {
-        const int h = i >> 4, d0 = (i & 15) * 8;
-        const uint16_t *qrow = p.query + (static_cast<size_t>(t) * kQueryHeads + h) * kHeadDim;
-        const half8_t q = rope ? rotate_chunk(qrow, d0, cos_row, sin_row) : *reinterpret_cast<const half8_t *>(qrow + d0);
-        *reinterpret_cast<half8_t *>(p.qrot + (static_cast<size_t>(t) * kQueryHeads + h) * kHeadDim + d0) = q;
-    }
-    if (i < 64) {
+    const uint32_t t = blockIdx.x * kAppendTokens + (i >> 6);
+    const int sub = i & 63;
+    if (t < p.tokens) {
+        bool rope = p.rope_cos != nullptr;
+        const int pos = p.positions ? p.positions[t] : static_cast<int>(t);
+        if (rope && (pos < 0 || static_cast<uint32_t>(pos) >= p.rope_rows)) {
+            if (sub == 0 && p.error_word) atomicOr(p.error_word, 4u);
+            rope = false;
+        }
+        const float *cos_row = rope ? p.rope_cos + static_cast<size_t>(pos) * 64 : nullptr;
+        const float *sin_row = rope ? p.rope_sin + static_cast<size_t>(pos) * 64 : nullptr;
         bool ok;
         const uint32_t blk = cache_block(p, t / kBlockTokens, &ok);
         if (!ok) {
-            if (i == 0 && p.error_word) atomicOr(p.error_word, 2u);
-            return;
-        }
-        const int hh = (i >> 4) & 1, c = i & 15, d0 = c * 8;
-        const size_t slab = (static_cast<size_t>(blk) * kKvHeads + hh) * kBlockHeadElems;
-        const uint32_t tt = t % kBlockTokens;
-        if (i < 32) {
-            const uint16_t *krow = p.key + (static_cast<size_t>(t) * kKvHeads + hh) * kHeadDim;
-            const half8_t k = rope ? rotate_chunk(krow, d0, cos_row, sin_row)
-                                   : *reinterpret_cast<const half8_t *>(krow + d0);
-            *reinterpret_cast<half8_t *>(p.key_cache + slab + c * 128 + key_slot(tt) * 8) = k;
+            if (sub == 0 && p.error_word) atomicOr(p.error_word, 2u);
         } else {
-            const u16x8_t v = *reinterpret_cast<const u16x8_t *>(p.value + (static_cast<size_t>(t) * kKvHeads + hh) *
-                                                                                    kHeadDim + d0);
+            const int hh = (sub >> 4) & 1, c = sub & 15, d0 = c * 8;
+            const size_t slab = (static_cast<size_t>(blk) * kKvHeads + hh) * kBlockHeadElems;
+            const uint32_t tt = t % kBlockTokens;
+            if (sub < 32) {
+                const uint16_t *krow = p.key + (static_cast<size_t>(t) * kKvHeads + hh) * kHeadDim;
+                const half8_t k = rope ? rotate_chunk(krow, d0, cos_row, sin_row)
+                                       : *reinterpret_cast<const half8_t *>(krow + d0);
+                *reinterpret_cast<half8_t *>(p.key_cache + slab + c * 128 + key_slot(static_cast<int>(tt)) * 8) = k;
+            } else {
+                const u16x8_t v = *reinterpret_cast<const u16x8_t *>(
+                    p.value + (static_cast<size_t>(t) * kKvHeads + hh) * kHeadDim + d0);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) p.value_cache[slab + (d0 + j) * kBlockTokens + tt] = v[j];
+                for (int j = 0; j < 8; ++j) p.value_cache[slab + (d0 + j) * kBlockTokens + tt] = v[j];
+            }
+        }
+    }
+    if (p.qrot) {
+        // (token, head, 8-dim chunk) items of the workgroup's tokens.
+        for (int k = i; k < kAppendTokens * kQueryHeads * 16; k += 256) {
+            const uint32_t tq = blockIdx.x * kAppendTokens + k / (kQueryHeads * 16);
+            if (tq >= p.tokens) break;
+            const int h = (k >> 4) % kQueryHeads, d0 = (k & 15) * 8;
+            const int pos = p.positions ? p.positions[tq] : static_cast<int>(tq);
+            const bool rope = p.rope_cos != nullptr && pos >= 0 && static_cast<uint32_t>(pos) < p.rope_rows;
+            const uint16_t *qrow = p.query + (static_cast<size_t>(tq) * kQueryHeads + h) * kHeadDim;
+            const half8_t q = rope ? rotate_chunk(qrow, d0, p.rope_cos + static_cast<size_t>(pos) * 64,
+                                                  p.rope_sin + static_cast<size_t>(pos) * 64)
+                                   : *reinterpret_cast<const half8_t *>(qrow + d0);
+            *reinterpret_cast<half8_t *>(p.qrot + (static_cast<size_t>(tq) * kQueryHeads + h) * kHeadDim + d0) = q;
         }
     }
 }
@@ -151,15 +169,45 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     const int t0 = qb * kQueryBlock;
     const int my_token = t0 + row;  // query token of this lane's column
 
-    // Query fragments (B operand): column = token t0 + row of head h.
+    // Query fragments (B operand): column = token t0 + row of head h, dims
+    // kb*32 + kg*8 .. +8, rotated here (rotate-half: the partner of chunk kb
+    // is chunk kb^2 of the same lane) exactly as rotate_chunk does.
+    const int tq = min(my_token, n - 1);
+    const int qpos = p.positions ? p.positions[tq] : tq;
+    const bool qrope = p.rope_cos != nullptr && qpos >= 0 && static_cast<uint32_t>(qpos) < p.rope_rows;
+    float4_t qc[2][2], qs[2][2];  // cos/sin of pairs hk*32 + kg*8 .. +8 (hk = kb & 1)
+    {
+        const float *cr = qrope ? p.rope_cos + static_cast<size_t>(qpos) * 64 : reinterpret_cast<const float *>(p.query);
+        const float *sr = qrope ? p.rope_sin + static_cast<size_t>(qpos) * 64 : reinterpret_cast<const float *>(p.query);
+#pragma unroll
+        for (int hk = 0; hk < 2; ++hk)
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+                qc[hk][f] = *reinterpret_cast<const float4_t *>(cr + hk * 32 + kg * 8 + f * 4);
+                qs[hk][f] = *reinterpret_cast<const float4_t *>(sr + hk * 32 + kg * 8 + f * 4);
+            }
+    }
     half8_t qf[2][4];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
         const int h = static_cast<int>(g) * kGroup + wave * 2 + ct;
-        const uint16_t *qrow = p.qrot + (static_cast<size_t>(min(my_token, n - 1)) * kQueryHeads + h) * kHeadDim;
+        const uint16_t *qrow = p.query + (static_cast<size_t>(tq) * kQueryHeads + h) * kHeadDim;
+        half8_t raw[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) raw[kb] = *reinterpret_cast<const half8_t *>(qrow + kb * 32 + kg * 8);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            const half8_t q = *reinterpret_cast<const half8_t *>(qrow + kb * 32 + kg * 8);
+            half8_t q = raw[kb];
+            if (qrope) {
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const float c = qc[kb & 1][jj >> 2][jj & 3];
+                    const float sn = qs[kb & 1][jj >> 2][jj & 3];
+                    const float x = static_cast<float>(raw[kb][jj]);
+                    const float y = static_cast<float>(raw[kb ^ 2][jj]);
+                    q[jj] = kb < 2 ? to_h(x * c + (-y) * sn) : to_h(x * c + y * sn);
+                }
+            }
             qf[ct][kb] = my_token < n ? q : half8_t{};
         }
     }
@@ -174,25 +222,26 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     __shared__ uint16_t sv[2][kStepElems];
     u16x8_t pk[4], pv[4];
     int koff[4], voff[4];
+    {
+        const int c = static_cast<int>(threadIdx.x);  // chunk of a tile: keys chunk*16 + slot, values dim*2 + half
+        const int kchunk = c >> 4, kslot = c & 15;
+        const int vdim = c >> 1, vhalf = c & 1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int c = static_cast<int>(threadIdx.x) + i * (kWaves * 64);  // chunk 0..1023 of the step
-        // keys: c = tile*256 + chunk*16 + slot
-        const int kt = c >> 8, kchunk = (c >> 4) & 15, kslot = c & 15;
-        koff[i] = lds_key_offset(kt >> 1, kchunk, kslot >> 3, kt & 1, kslot & 7);
-        // values: c = tile*256 + dim*2 + half
-        const int vt = c >> 8, vdim = (c >> 1) & 127, vhalf = c & 1;
-        voff[i] = lds_value_offset(vt >> 1, vt & 1, vhalf, vdim);
+        for (int i = 0; i < 4; ++i) {  // tile i of the step
+            koff[i] = lds_key_offset(i >> 1, kchunk, kslot >> 3, i & 1, kslot & 7);
+            voff[i] = lds_value_offset(i >> 1, i & 1, vhalf, vdim);
+        }
     }
+    // Thread t moves 16-byte chunk t of each of the step's 4 tiles (the
+    // tile index is uniform, so the block-table read is a scalar load).
     auto gload = [&](int step) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int c = static_cast<int>(threadIdx.x) + i * (kWaves * 64);
             bool ok;
-            const uint32_t blk = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + (c >> 8), last_tile)), &ok);
+            const uint32_t blk = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + i, last_tile)), &ok);
             const size_t slab = (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems;
-            pk[i] = *reinterpret_cast<const u16x8_t *>(p.key_cache + slab + (c & 255) * 8);
-            pv[i] = *reinterpret_cast<const u16x8_t *>(p.value_cache + slab + (c & 255) * 8);
+            pk[i] = *reinterpret_cast<const u16x8_t *>(p.key_cache + slab + threadIdx.x * 8);
+            pv[i] = *reinterpret_cast<const u16x8_t *>(p.value_cache + slab + threadIdx.x * 8);
         }
     };
     auto lstore = [&](int buf) {
@@ -347,7 +396,8 @@ int launch_prefill(const pvlc_hip_paged_prefill_args *a, void *stream) {
     p.error_word = a->error_word;
     p.scale_log2 = kLog2e / sqrtf(static_cast<float>(kHeadDim));
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(prefill_rope_append_kernel, dim3(a->tokens), dim3(256), 0, st, p);
+    hipLaunchKernelGGL(prefill_rope_append_kernel, dim3((a->tokens + kAppendTokens - 1) / kAppendTokens), dim3(256), 0,
+                       st, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     const unsigned qblocks = (a->tokens + kQueryBlock - 1) / kQueryBlock;

@@ -540,8 +540,7 @@ pvlc_hip_status pvlc_hip_paged_prefill_f16(const pvlc_hip_paged_prefill_args *ar
     if (!args) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill args are NULL");
     if (args->tokens == 0 || args->num_blocks == 0)
         return invalid(PVLC_HIP_INV_ZERO_DIMENSION, "tokens and blocks must be nonzero");
-    if (!args->query || !args->key || !args->value || !args->out || !args->key_cache || !args->value_cache ||
-        !args->query_scratch)
+    if (!args->query || !args->key || !args->value || !args->out || !args->key_cache || !args->value_cache)
         return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill buffer pointer is NULL");
     if ((args->rope_cos == nullptr) != (args->rope_sin == nullptr) || (args->rope_cos && args->rope_rows == 0))
         return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION, "rotary tables must be given together with rows");
