@@ -337,7 +337,10 @@ uint32_t pvlc_hip_paged_decode_partition(uint32_t num_seqs, uint32_t max_context
 size_t pvlc_hip_paged_decode_workspace_bytes(uint32_t num_seqs, uint32_t max_context, uint32_t partition_tokens);
 /* Zero a workspace on `stream` (a fill kernel; safe under graph capture). */
 pvlc_hip_status pvlc_hip_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
-/* Device error word of a workspace (0 = no clamped access); synchronises. */
+/* Device error word of a workspace (0 = none); synchronises.  Bits: 1 = a
+ * cache length with no room for the append (sequence skipped), 2 = a block id
+ * outside the planes (block 0 read, the appended row not written), 4 = a
+ * rotary position outside the tables (no rotation). */
 pvlc_hip_status pvlc_hip_workspace_error(const void *workspace, size_t workspace_bytes, void *stream,
                                          uint32_t *error_out);
 

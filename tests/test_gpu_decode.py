@@ -182,7 +182,8 @@ def test_wrong_grouping_would_be_detected(runtime):
     assert np.max(np.abs(out - wrong)) > 0.05
 
 
-def device_decode(layers, prefix, capacity, seed, rope=True, rotate_query=False, partition=0, positions=None):
+def device_decode(layers, prefix, capacity, seed, rope=True, rotate_query=False, partition=0, positions=None,
+                  workspace=None):
     """Contiguous per-layer caches (block_tables NULL), one launch for all layers."""
     import torch
     nb_per = (capacity + 15) // 16
@@ -204,9 +205,12 @@ def device_decode(layers, prefix, capacity, seed, rope=True, rotate_query=False,
     d_out = torch.zeros(layers * 2048, dtype=torch.int16, device="cuda")
     d_cos, d_sin = to_dev_f32(cos), to_dev_f32(sin)
     d_pos = to_dev_i32(positions) if positions is not None else None
-    wsb = pvlc.decode_workspace_bytes(layers, capacity, partition)
-    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
-    pvlc.workspace_init(ws, wsb)
+    if workspace is None:
+        wsb = pvlc.decode_workspace_bytes(layers, capacity, partition)
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        pvlc.workspace_init(ws, wsb)
+    else:
+        ws, wsb = workspace
     args = pvlc.paged_decode_args(num_seqs=layers, num_blocks=layers * nb_per, max_blocks_per_seq=nb_per,
                                   key_cache=d_k, value_cache=d_v, query=d_q, new_key=d_nk, new_value=d_nv,
                                   out=d_out, workspace=ws, workspace_bytes=wsb, max_context=capacity,
@@ -266,7 +270,7 @@ def test_no_rotary_small_contexts():
         check_device_layers(r, 2, prefix, rope=False, label=f"norope p={prefix}")
 
 
-def paged_case(num_seqs, lo, hi, seed, partition=0, log_uniform=False):
+def paged_case(num_seqs, lo, hi, seed, partition=0, log_uniform=False, workspace=None):
     """Ragged batch over a shared paged cache with seeded permuted block tables."""
     import torch
     rng = np.random.default_rng(seed)
@@ -299,9 +303,12 @@ def paged_case(num_seqs, lo, hi, seed, partition=0, log_uniform=False):
     cos, sin = pvlc.rope_table(500000.0, max_context + 1)
     d_k, d_v = to_dev(kp), to_dev(vp)
     d_out = torch.zeros(num_seqs * 2048, dtype=torch.int16, device="cuda")
-    wsb = pvlc.decode_workspace_bytes(num_seqs, max_context, partition)
-    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
-    pvlc.workspace_init(ws, wsb)
+    if workspace is None:
+        wsb = pvlc.decode_workspace_bytes(num_seqs, max_context, partition)
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        pvlc.workspace_init(ws, wsb)
+    else:
+        ws, wsb = workspace
     keep = [to_dev(q), to_dev(nk), to_dev(nv), to_dev_i32(tables), to_dev_i32(cache_lens), to_dev_f32(cos),
             to_dev_f32(sin)]
     args = pvlc.paged_decode_args(num_seqs=num_seqs, num_blocks=num_blocks, max_blocks_per_seq=max_blocks,
@@ -332,6 +339,24 @@ def test_paged_ragged_batch(partition):
 def test_paged_long_context_split_k():
     log("case: paged long context (8 seqs, log-uniform [1024, 9000], partition 512)")
     paged_case(8, 1024, 9000, seed=950, partition=512, log_uniform=True)
+
+
+def test_one_workspace_across_launch_paths_and_partitions():
+    # The split-K merge relies on the workspace's sentinels; every launch must restore them, whichever path
+    # (single-shot in-kernel merge or streaming partials + merge kernel) and partition stride it used.
+    import torch
+    wsb = max(pvlc.decode_workspace_bytes(18, 2304, p) for p in (0, 64, 512))
+    wsb = max(wsb, pvlc.decode_workspace_bytes(12, 3000, 0), pvlc.decode_workspace_bytes(12, 3000, 64))
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    pvlc.workspace_init(ws, wsb)
+    for i, (kind, part) in enumerate([("uniform", 0), ("ragged", 0), ("uniform", 64), ("uniform", 0),
+                                      ("ragged", 64), ("uniform", 512), ("uniform", 0)]):
+        log(f"case: shared workspace launch {i}: {kind} partition={part}")
+        if kind == "uniform":
+            r = device_decode(18, 2047, 2304, seed=1200 + i, partition=part, workspace=(ws, wsb))
+            check_device_layers(r, 18, 2047, label=f"shared ws {i}")
+        else:
+            paged_case(12, 1, 3000, seed=1300 + i, partition=part, workspace=(ws, wsb))
 
 
 def test_pack_unpack_roundtrip_through_block_table():
