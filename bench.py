@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                     help="2 = headline 18-layer step (default); 3 = paged ragged batch; 4 = causal prefill; "
                          "5 = long-context split-K batch")
+    ap.add_argument("--gemv", action="store_true",
+                    help="decoder weight GEMVs of one token step (18 layers x 7 projections + LM head, fp16 weights)")
     return ap.parse_args()
 
 
@@ -75,6 +77,8 @@ def main() -> int:
         return 2
     if args.calibrate_copy:
         return calibrate_copy(args)
+    if args.gemv:
+        return bench_gemv(args)
     if args.config == 4:
         return bench_prefill(args)
     if args.config in (3, 5):
@@ -363,6 +367,154 @@ def bench_prefill(args):
                                                  "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4)}},
         ensure_ascii=False))
     return 0
+
+
+# Decoder projections of one layer, rows x columns (gemv_tiled_plan_contract.rs and
+# decoder_stack_tiled_gemv_web_module_contract.rs:721-757), in the order the reference
+# session dispatches them; the LM head follows the last layer.
+GEMV_LAYER = (("q", 2048, 1024), ("k", 256, 1024), ("v", 256, 1024), ("o", 1024, 2048),
+              ("gate", 3072, 1024), ("up", 3072, 1024), ("down", 1024, 3072))
+GEMV_HEAD = ("lm_head", 103_424, 1024)
+
+
+def gemv_bytes(rows, columns):
+    """fp16 weights once + f32 input vector + f32 output."""
+    return rows * columns * 2 + columns * 4 + rows * 4
+
+
+def bench_gemv(args):
+    """Weight GEMVs of one decoder token step: 18 layers x (q, k, v, o, gate, up, down) + LM head, each layer
+    with its own weights (721 MB per step, so every step streams them from HBM).  Also reported: the same
+    bytes in 4 launches per layer (q|k|v and gate|up as one weight matrix each, rows concatenated), and each
+    projection shape alone over enough weight copies to stay out of the Infinity Cache."""
+    import torch
+
+    from __graft_entry__ import load_package
+
+    pvlc = load_package()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device=dev).manual_seed(11)
+
+    def weights(rows, columns):
+        return (torch.randn(rows * columns, generator=gen, device=dev) * 0.02).half()
+
+    def vec(n):
+        return torch.randn(n, generator=gen, device=dev)
+
+    inputs = {c: vec(c) for c in (1024, 2048, 3072)}
+    outs = {}
+    separate, fused = [], []
+    for layer in range(LAYERS):
+        qkv = weights(2560, 1024)
+        gate_up = weights(6144, 1024)
+        w = {"q": qkv[:2048 * 1024], "k": qkv[2048 * 1024:2304 * 1024], "v": qkv[2304 * 1024:],
+             "gate": gate_up[:3072 * 1024], "up": gate_up[3072 * 1024:],
+             "o": weights(1024, 2048), "down": weights(1024, 3072)}
+        for name, rows, columns in GEMV_LAYER:
+            out = outs.setdefault((name, rows), torch.empty(rows, device=dev))
+            separate.append((w[name], inputs[columns], out, rows, columns))
+        fused += [(qkv, inputs[1024], outs.setdefault(("qkv", 2560), torch.empty(2560, device=dev)), 2560, 1024),
+                  (w["o"], inputs[2048], outs[("o", 1024)], 1024, 2048),
+                  (gate_up, inputs[1024], outs.setdefault(("gate_up", 6144), torch.empty(6144, device=dev)),
+                   6144, 1024),
+                  (w["down"], inputs[3072], outs[("down", 1024)], 1024, 3072)]
+    head_w = weights(GEMV_HEAD[1], GEMV_HEAD[2])
+    logits = torch.empty(GEMV_HEAD[1], device=dev)
+    separate.append((head_w, inputs[1024], logits, GEMV_HEAD[1], GEMV_HEAD[2]))
+    fused.append(separate[-1])
+    step_bytes = sum(gemv_bytes(r, c) for _, _, _, r, c in separate)
+    fused_bytes = sum(gemv_bytes(r, c) for _, _, _, r, c in fused)
+
+    def step(calls):
+        for w_, x_, o_, r_, c_ in calls:
+            pvlc.gemv_f16(w_, x_, o_, r_, c_, stream)
+
+    torch.cuda.synchronize()
+    if args.profile_steps:
+        for _ in range(args.profile_steps):
+            step(separate)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_steps": args.profile_steps, "launches_per_step": len(separate)}))
+        return 0
+    for _ in range(args.warmup):
+        step(separate)
+        step(fused)
+    steps = min(args.steps, 100)
+    ms = _timed_launches(torch, stream, steps, lambda i: step(separate))
+    ms_fused = _timed_launches(torch, stream, steps, lambda i: step(fused))
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    gbps_fused = fused_bytes / (ms_fused * 1e-3) / 1e9
+
+    # each shape alone: rotate over copies totalling >= 768 MB so reads come from HBM
+    shapes = {}
+    for name, rows, columns in (("q", 2048, 1024), ("k|v", 256, 1024), ("o", 1024, 2048), ("gate|up", 3072, 1024),
+                                ("down", 1024, 3072), GEMV_HEAD, ("q+k+v", 2560, 1024), ("gate+up", 6144, 1024)):
+        copies = max(2, -(-(768 << 20) // (rows * columns * 2)))
+        ws = [weights(rows, columns) for _ in range(copies)]
+        out = torch.empty(rows, device=dev)
+        fn = lambda i: pvlc.gemv_f16(ws[i % copies], inputs[columns], out, rows, columns, stream)
+        for i in range(copies):
+            fn(i)
+        k = max(copies * 2, 50)
+        t = _timed_launches(torch, stream, k, fn)
+        shapes[f"{name} {rows}x{columns}"] = {"us": round(t * 1e3, 2),
+                                              "gbps": round(gemv_bytes(rows, columns) / (t * 1e-3) / 1e9, 1)}
+        del ws
+    torch.cuda.synchronize()
+
+    result = {
+        "metric": "decoder weight-GEMV step µs + achieved HBM GB/s (18 layers x 7 projections + LM head)",
+        "value": round(ms * 1e3, 2), "unit": "µs/step", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": False, "dtype": "f16 weights, f32 vector/accumulate",
+        "data": "synthetic N(0,1)*0.02 fp16 weights, N(0,1) f32 vectors, seeded",
+        "config": {"workload": "one decoder token step's weight GEMVs: 18 x (q 2048x1024, k/v 256x1024, o 1024x2048, "
+                               "gate/up 3072x1024, down 1024x3072) + LM head 103424x1024, each layer its own weights",
+                   "launches_per_step": len(separate)},
+        "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_step": step_bytes},
+        "rows_concatenated": {"launches_per_step": len(fused), "us": round(ms_fused * 1e3, 2),
+                              "gbps": round(gbps_fused, 1), "pct_hbm_peak": round(100 * gbps_fused / HBM_PEAK_GBPS, 2)},
+        "per_shape_hbm": shapes,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = gemv_cpu_baseline(separate, logits, args.cpu_seconds, step_bytes)
+    print(json.dumps(result, ensure_ascii=False))
+    return 0
+
+
+def gemv_cpu_baseline(calls, logits, seconds, step_bytes):
+    """linear_f32 of pvlc-cpu-ref restated in C (oracle/), single thread, zero bias, on the same fp16 weights
+    widened to f32: the last layer's seven projections plus the LM head, repeated for a bounded time, scaled to
+    one 18-layer step."""
+    import oracle as O
+
+    host = []
+    for w_, x_, o_, r_, c_ in calls[-8:]:
+        host.append((w_.float().cpu().numpy(), x_.cpu().numpy(), r_, c_))
+    zero = {r: np.zeros(r, np.float32) for _, _, r, _ in host}
+    layer_t, head_t, reps = 0.0, 0.0, 0
+    t_end = time.perf_counter() + seconds
+    head_out = None
+    while time.perf_counter() < t_end or reps == 0:
+        t0 = time.perf_counter()
+        for wf, x, r, c in host[:-1]:
+            O.linear_f32(x, 1, c, wf, zero[r], r)
+        t1 = time.perf_counter()
+        wf, x, r, c = host[-1]
+        head_out = O.linear_f32(x, 1, c, wf, zero[r], r)
+        layer_t += t1 - t0
+        head_t += time.perf_counter() - t1
+        reps += 1
+    per_step = LAYERS * layer_t / reps + head_t / reps
+    max_err = float(np.max(np.abs(logits.cpu().numpy() - head_out)))
+    return {"value": round(per_step * 1e6, 1), "unit": "µs/step", "cores": 1, "kind": "port",
+            "gbps": round(step_bytes / per_step / 1e9, 3),
+            "sample": f"{reps} x (one layer's 7 GEMVs + LM head), scaled to 18 layers + head "
+                      f"({layer_t + head_t:.1f} s)",
+            "gpu_vs_cpu_logits_max_abs": max_err}
 
 
 def cpu_baseline(host_q, host_k, host_v, host_nk, host_nv, cos, sin, seconds, step_bytes, gpu_out):

@@ -387,6 +387,39 @@ pvlc_hip_status pvlc_hip_kv_unpack_f16(const uint16_t *key_cache, const uint16_t
                                        const int32_t *block_table, uint32_t num_blocks, uint16_t *key_rows,
                                        uint16_t *value_rows, void *stream);
 
+/* ---------------------------------------------------------------------------
+ * Decoder GEMV with fp16 weights (the next path widened from this backend).
+ * ------------------------------------------------------------------------- */
+
+/* GemvTiledPlan, runtime-core lib.rs:729-745 (the reference's tiled GEMV
+ * lattice: 8 rows x 32 lanes per 256-thread workgroup, vec4 columns). */
+typedef struct pvlc_hip_gemv_tiled_plan {
+    uint32_t tile_rows;
+    uint32_t threads_per_row;
+    uint32_t vector_width;
+    uint32_t shared_capacity;
+    uint32_t workgroup_storage_bytes;
+    uint32_t dispatch[3];
+    uint32_t workgroup_size[3];
+    uint32_t uniform_words[4];
+    uint64_t output_elements;
+    uint64_t output_bytes;
+} pvlc_hip_gemv_tiled_plan;
+
+/* GemvTiledDescriptor::plan, runtime-core lib.rs:753-785: nonzero rows, the
+ * decoder input widths 1024/2048/3072, at most 8 x 65535 rows. */
+pvlc_hip_status pvlc_hip_gemv_tiled_plan_create(uint32_t rows, uint32_t columns, pvlc_hip_gemv_tiled_plan *plan_out);
+
+/* out[r] = sum_c weights[r][c] * vector[c] for r < rows: fp16 weights,
+ * output-major [rows][columns]; f32 vector and output; f32 accumulation.
+ * Device pointers, caller stream, no allocation, no synchronisation; the
+ * geometry is admitted exactly as the plan above.  Replaces
+ * gemv_tiled_f16_weights (pvlc-wgsl lib.rs:1770-1835) in the seven per-layer
+ * projections and the LM head (decoder_stack_session.rs; web module contract
+ * decoder_stack_tiled_gemv_web_module_contract.rs). */
+pvlc_hip_status pvlc_hip_gemv_f16(const uint16_t *weights, const float *vector, float *out, uint32_t rows,
+                                  uint32_t columns, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

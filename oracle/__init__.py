@@ -69,6 +69,7 @@ def _declare(l: ctypes.CDLL) -> None:
     l.oracle_decode_gqa_f32.argtypes = [_F, _SZ, _F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, _SZ, _F]
     l.oracle_causal_gqa_f32.argtypes = [_F, _SZ, _F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, _SZ, _F]
     l.oracle_append_kv_f32.argtypes = [_F, _F, _SZ, _F, _SZ, _F, _SZ, _SZ, _SZ, _F, _F]
+    l.oracle_linear_f32.argtypes = [_F, _SZ, _SZ, _SZ, _F, _SZ, _F, _SZ, _SZ, _F]
     l.oracle_write_prefill_kv_f32.argtypes = [_F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, _F, _F]
     l.oracle_rope_neox_f32.argtypes = [_F, _SZ, _SZ, _SZ, _SZ, _U32, _SZ, ctypes.c_float]
     l.oracle_mrope_f32.argtypes = [_F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, _SZ, _F, _F, _SZ,
@@ -117,6 +118,15 @@ def causal_gqa_f32(query, key, value, tokens, query_heads, key_value_heads, head
     _check(lib().oracle_causal_gqa_f32(_ptr(q, _F), q.size, _ptr(k, _F), k.size, _ptr(v, _F), v.size,
                                        tokens, query_heads, key_value_heads, head_dim, _ptr(out, _F)))
     return out[: q.size]
+
+
+def linear_f32(input, rows, input_width, weights, bias, output_width) -> np.ndarray:
+    """linear_f32 (cpu-ref lib.rs:131-140 via patch_projection_f32 :88-128)."""
+    x, w, b = _f32(input).ravel(), _f32(weights).ravel(), _f32(bias).ravel()
+    out = np.zeros(max(rows * output_width, 1), dtype=np.float32)
+    _check(lib().oracle_linear_f32(_ptr(x, _F), x.size, rows, input_width, _ptr(w, _F), w.size, _ptr(b, _F),
+                                   b.size, output_width, _ptr(out, _F)))
+    return out[: rows * output_width]
 
 
 def append_kv_f32(prefix_keys, prefix_values, prefix_tokens, rotated_key, value, key_value_heads, head_dim):

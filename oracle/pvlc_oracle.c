@@ -189,6 +189,33 @@ int oracle_append_kv_f32(const float *prefix_keys, const float *prefix_values, s
     return ORACLE_OK;
 }
 
+int oracle_linear_f32(const float *input, size_t input_len, size_t rows, size_t input_width,
+                      const float *weights, size_t weights_len, const float *bias, size_t bias_len,
+                      size_t output_width, float *out) {
+    /* patch_projection_f32 validation order (lib.rs:97-111), patch_size 1 */
+    if (rows == 0 || input_width == 0 || output_width == 0) return ORACLE_DIMENSION_MISMATCH;
+    int rc = require_len(input_len, rows, input_width);
+    if (rc != ORACLE_OK) return rc;
+    rc = require_len(weights_len, output_width, input_width);
+    if (rc != ORACLE_OK) return rc;
+    if (bias_len != output_width) return ORACLE_DIMENSION_MISMATCH;
+    if (!all_finite(input, input_len) || !all_finite(weights, weights_len) || !all_finite(bias, bias_len))
+        return ORACLE_NON_FINITE_INPUT;
+    size_t out_len;
+    if (!checked_mul(rows, output_width, &out_len)) return ORACLE_DIMENSION_MISMATCH;
+    /* lib.rs:117-126: accumulator starts at the bias, += input * coefficient in order */
+    for (size_t r = 0; r < rows; ++r) {
+        const float *patch = input + r * input_width;
+        for (size_t o = 0; o < output_width; ++o) {
+            const float *w = weights + o * input_width;
+            float accumulator = bias[o];
+            for (size_t i = 0; i < input_width; ++i) accumulator += patch[i] * w[i];
+            out[r * output_width + o] = accumulator;
+        }
+    }
+    return ORACLE_OK;
+}
+
 int oracle_write_prefill_kv_f32(const float *rotated_key, size_t key_len, const float *value,
                                 size_t value_len, size_t tokens, size_t key_value_heads, size_t head_dim,
                                 float *out_keys, float *out_values) {

@@ -24,6 +24,9 @@
  *                           selection checked against a brute-force table.
  *   oracle_f32_to_f16       exhaustive comparison with numpy's RNE float16 cast.
  *   oracle_blake3           BLAKE3 specification test vectors, model-lock digests.
+ *   oracle_linear_f32       the reference's known answer (vision_contract.rs:433-441),
+ *                           its error cases (:444-470), exact small-integer
+ *                           products against numpy, an f64 bound.
  */
 #ifndef PVLC_ORACLE_H
 #define PVLC_ORACLE_H
@@ -56,6 +59,13 @@ int oracle_decode_gqa_f32(const float *query, size_t query_len, const float *key
 int oracle_causal_gqa_f32(const float *query, size_t query_len, const float *key, size_t key_len,
                           const float *value, size_t value_len, size_t tokens, size_t query_heads,
                           size_t key_value_heads, size_t head_dim, float *out);
+
+/* linear_f32 = patch_projection_f32 with patch_size 1, lib.rs:88-128, 131-140:
+ * out[r][o] = bias[o] + sum_i input[r][i] * weights[o][i], accumulated in
+ * input order from the bias.  weights are output-major [output_width][input_width]. */
+int oracle_linear_f32(const float *input, size_t input_len, size_t rows, size_t input_width,
+                      const float *weights, size_t weights_len, const float *bias, size_t bias_len,
+                      size_t output_width, float *out);
 
 /* append_decoder_kv_cache, lib.rs:1420-1450: out = prefix rows || one new row. */
 int oracle_append_kv_f32(const float *prefix_keys, const float *prefix_values, size_t prefix_tokens,

@@ -97,6 +97,12 @@ class GqaSplitPlanC(ctypes.Structure):
                 ("merge_workgroups", _U32), ("uniform_words", _U32 * 4)]
 
 
+class GemvTiledPlanC(ctypes.Structure):
+    _fields_ = [("tile_rows", _U32), ("threads_per_row", _U32), ("vector_width", _U32), ("shared_capacity", _U32),
+                ("workgroup_storage_bytes", _U32), ("dispatch", _U32 * 3), ("workgroup_size", _U32 * 3),
+                ("uniform_words", _U32 * 4), ("output_elements", ctypes.c_uint64), ("output_bytes", ctypes.c_uint64)]
+
+
 class KvStepPlanC(ctypes.Structure):
     _fields_ = [("cache_tokens_before", _U32), ("cache_tokens_after", _U32),
                 ("valid_cache_elements", ctypes.c_uint64), ("append_uniform_words", _U32 * 4),
@@ -182,6 +188,8 @@ SIGNATURES = {
     "pvlc_hip_paged_prefill_f16": ([ctypes.POINTER(PagedPrefillArgsC), _VP], ctypes.c_int32),
     "pvlc_hip_kv_pack_f16": ([_VP, _VP, _U32, _VP, _U32, _VP, _VP, _VP], ctypes.c_int32),
     "pvlc_hip_kv_unpack_f16": ([_VP, _VP, _U32, _VP, _U32, _VP, _VP, _VP], ctypes.c_int32),
+    "pvlc_hip_gemv_tiled_plan_create": ([_U32, _U32, ctypes.POINTER(GemvTiledPlanC)], ctypes.c_int32),
+    "pvlc_hip_gemv_f16": ([_VP, _VP, _VP, _U32, _U32, _VP], ctypes.c_int32),
 }
 
 
@@ -351,6 +359,19 @@ def plan_gqa_split(cache_tokens: int, query_heads: int = QUERY_HEADS, key_value_
     _check(lib.pvlc_hip_gqa_split_plan_create(cache_tokens, query_heads, key_value_heads, head_dim,
                                               ctypes.byref(out)))
     return _struct_dict(out)
+
+
+def plan_gemv_tiled(rows: int, columns: int) -> dict:
+    """GemvTiledDescriptor::plan (runtime-core lib.rs:753-785)."""
+    out = GemvTiledPlanC()
+    _check(lib.pvlc_hip_gemv_tiled_plan_create(rows, columns, ctypes.byref(out)))
+    return _struct_dict(out)
+
+
+def gemv_f16(weights, vector, out, rows: int, columns: int, stream=None) -> None:
+    """out[r] = sum_c weights[r][c] * vector[c] (fp16 weights, f32 vector and output): replaces
+    gemv_tiled_f16_weights (pvlc-wgsl lib.rs:1770-1835); admission as plan_gemv_tiled."""
+    _check(lib.pvlc_hip_gemv_f16(_ptr(weights), _ptr(vector), _ptr(out), rows, columns, _stream(stream)))
 
 
 def plan_prefill(tokens: int, cache_capacity: int) -> None:

@@ -318,6 +318,36 @@ DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts) {
     return w;
 }
 
+int plan_gemv_tiled(uint32_t rows, uint32_t columns, pvlc_hip_gemv_tiled_plan *out) {
+    // runtime-core lib.rs:746-785
+    constexpr uint32_t kTileRows = 8, kThreadsPerRow = 32, kVectorWidth = 4;
+    constexpr uint32_t kSharedCapacity = 3072, kStorageBytes = 13312, kMaxDispatch = 65535;
+    if (rows == 0 || !(columns == 1024 || columns == 2048 || columns == 3072))
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY,
+                       "tiled decoder GEMV geometry " + std::to_string(rows) + "x" + std::to_string(columns) +
+                           " is outside the admitted nonzero rows and 1024/2048/3072 input widths");
+    const uint32_t dispatch_x = rows / kTileRows + (rows % kTileRows != 0);
+    if (dispatch_x > kMaxDispatch)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY,
+                       "tiled decoder GEMV rows " + std::to_string(rows) + " exceed the single-dispatch workgroup bound");
+    pvlc_hip_gemv_tiled_plan p{};
+    p.tile_rows = kTileRows;
+    p.threads_per_row = kThreadsPerRow;
+    p.vector_width = kVectorWidth;
+    p.shared_capacity = kSharedCapacity;
+    p.workgroup_storage_bytes = kStorageBytes;
+    p.dispatch[0] = dispatch_x;
+    p.dispatch[1] = p.dispatch[2] = 1;
+    p.workgroup_size[0] = 256;
+    p.workgroup_size[1] = p.workgroup_size[2] = 1;
+    p.uniform_words[0] = rows;
+    p.uniform_words[1] = columns;
+    p.output_elements = rows;
+    p.output_bytes = static_cast<uint64_t>(rows) * 4;
+    if (out) *out = p;
+    return ok();
+}
+
 DecodeShape decode_shape(uint32_t partition_tokens, bool streaming) {
     const uint32_t tiles = (partition_tokens + kBlockTokens - 1) / kBlockTokens;
     if (streaming) return tiles >= 8 ? DecodeShape{4, 1} : DecodeShape{2, 1};
@@ -379,6 +409,11 @@ uint32_t auto_workspace_parts(uint32_t num_seqs, uint32_t max_context) {
 using namespace pvlc;
 
 extern "C" {
+
+pvlc_hip_status pvlc_hip_gemv_tiled_plan_create(uint32_t rows, uint32_t columns, pvlc_hip_gemv_tiled_plan *plan_out) {
+    if (!plan_out) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "plan output is NULL");
+    return plan_gemv_tiled(rows, columns, plan_out);
+}
 
 const char *pvlc_hip_last_error_message(void) { return g_last_error.c_str(); }
 

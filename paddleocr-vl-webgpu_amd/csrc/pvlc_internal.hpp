@@ -97,6 +97,11 @@ int launch_kv_pack(const uint16_t *key_rows, const uint16_t *value_rows, uint32_
 int launch_kv_unpack(const uint16_t *key_cache, const uint16_t *value_cache, uint32_t tokens, const int32_t *table,
                      uint32_t num_blocks, uint16_t *key_rows, uint16_t *value_rows, void *stream);
 int launch_prefill(const pvlc_hip_paged_prefill_args *args, void *stream);
+int launch_gemv_f16(const uint16_t *weights, const float *vector, float *out, uint32_t rows, uint32_t columns,
+                    void *stream);
+
+// GemvTiledDescriptor::plan (runtime-core lib.rs:753-785); returns a status.
+int plan_gemv_tiled(uint32_t rows, uint32_t columns, pvlc_hip_gemv_tiled_plan *out);
 
 // Workspace layout of the paged decode.
 struct DecodeWorkspace {

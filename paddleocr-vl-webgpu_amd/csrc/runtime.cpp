@@ -477,6 +477,15 @@ uint32_t pvlc_hip_paged_decode_partition(uint32_t num_seqs, uint32_t max_context
     return auto_partition(num_seqs, max_context);
 }
 
+pvlc_hip_status pvlc_hip_gemv_f16(const uint16_t *weights, const float *vector, float *out, uint32_t rows,
+                                  uint32_t columns, void *stream) {
+    if (!weights || !vector || !out) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "GEMV buffer pointer is NULL");
+    if (pvlc_hip_status st = plan_gemv_tiled(rows, columns, nullptr)) return st;
+    const int e = launch_gemv_f16(weights, vector, out, rows, columns, stream);
+    if (e != 0) return hip_fail(static_cast<hipError_t>(e), "GEMV launch");
+    return ok();
+}
+
 size_t pvlc_hip_paged_decode_workspace_bytes(uint32_t num_seqs, uint32_t max_context, uint32_t partition_tokens) {
     if (num_seqs == 0 || max_context == 0) return 0;
     if (partition_tokens == 0) return decode_workspace_layout(num_seqs, auto_workspace_parts(num_seqs, max_context)).total;

@@ -98,3 +98,17 @@ def from_dev(t):
 def log(msg):
     print(msg, flush=True)
     sys.stdout.flush()
+
+
+def dot_error_ratio(got, weights, x, chain):
+    """max over rows of |got - W.x (f64)| / (gamma_chain * sum|W*x|): the standard error bound of an f32 dot
+    product whose output passes through `chain` roundings (gamma_m = m*u/(1-m*u), u = 2^-24); <= 1 holds for
+    any evaluation order of that depth."""
+    u = 2.0 ** -24
+    g = chain * u / (1 - chain * u)
+    w64 = np.asarray(weights, np.float64)
+    x64 = np.asarray(x, np.float64)
+    exact = w64 @ x64
+    mag = np.abs(w64) @ np.abs(x64)
+    err = np.abs(np.asarray(got, np.float64) - exact)
+    return float((err / np.maximum(g * mag, 1e-300)).max())

@@ -363,3 +363,48 @@ def test_write_prefill_kv_is_a_validated_clone():
     with pytest.raises(O.OracleError) as err:
         O.write_prefill_kv_f32(k, v, 0, kvh, hd)
     assert err.value.code == "DimensionMismatch"
+
+
+def test_linear_reproduces_reference_known_answer():
+    # crates/pvlc-cpu-ref/tests/vision_contract.rs:433-441 (output-major weights, bias added first)
+    out = O.linear_f32([1.0, 2.0, 3.0, -1.0, 0.0, 2.0], 2, 3, [1.0, 2.0, 3.0, -1.0, 0.5, 2.0], [0.25, -0.5], 2)
+    np.testing.assert_array_equal(out, np.array([14.25, 5.5, 5.25, 4.5], np.float32))
+
+
+def test_linear_validation_errors_follow_reference():
+    # vision_contract.rs:444-470: zero dimensions and length mismatches, then non-finite operands
+    for rows, width, out_w in [(0, 3, 2), (2, 0, 2), (2, 3, 0)]:
+        with pytest.raises(O.OracleError) as err:
+            O.linear_f32([], rows, width, [], [], out_w)
+        assert err.value.code == "DimensionMismatch"
+    for x, w, b in [([1.0, 2.0], [1.0, 2.0, 3.0], [0.0]), ([1.0, 2.0, 3.0], [1.0, 2.0], [0.0]),
+                    ([1.0, 2.0, 3.0], [1.0, 2.0, 3.0], [])]:
+        with pytest.raises(O.OracleError) as err:
+            O.linear_f32(x, 1, 3, w, b, 1)
+        assert err.value.code == "DimensionMismatch"
+    for x, w, b in [([1.0, np.nan, 3.0], [1.0, 2.0, 3.0], [0.0]), ([1.0, 2.0, 3.0], [1.0, np.inf, 3.0], [0.0]),
+                    ([1.0, 2.0, 3.0], [1.0, 2.0, 3.0], [np.nan])]:
+        with pytest.raises(O.OracleError) as err:
+            O.linear_f32(x, 1, 3, w, b, 1)
+        assert err.value.code == "NonFiniteInput"
+
+
+def test_linear_is_exact_on_small_integers_and_within_f64_bound():
+    rng = np.random.default_rng(3)
+    # small integers: every partial sum is exactly representable, so any order is exact
+    x = rng.integers(-8, 9, (3, 1024)).astype(np.float32)
+    w = rng.integers(-8, 9, (40, 1024)).astype(np.float32)
+    b = rng.integers(-8, 9, 40).astype(np.float32)
+    out = O.linear_f32(x, 3, 1024, w, b, 40).reshape(3, 40)
+    want = (x.astype(np.int64) @ w.astype(np.int64).T + b.astype(np.int64)).astype(np.float32)
+    np.testing.assert_array_equal(out, want)
+    # general values: sequential f32 sum within the classical bound n*eps*sum|terms| of the f64 result
+    x = O.normal_f32(61, 2048)
+    w = O.f16_to_f32(O.normal_f16(62, 64 * 2048))
+    out = O.linear_f32(x, 1, 2048, w, np.zeros(64, np.float32), 64)
+    wm = w.reshape(64, 2048).astype(np.float64)
+    exact = wm @ x.astype(np.float64)
+    bound = 2048 * 2.0 ** -24 * (np.abs(wm) @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(out - exact) <= bound)
+    # a dropped term or a transposed weight layout would not pass
+    assert np.max(np.abs(out - (w.reshape(2048, 64).astype(np.float64).T @ x))) > 1.0
