@@ -432,10 +432,18 @@ def bench_gemv(args):
 
     torch.cuda.synchronize()
     if args.profile_steps:
+        # the step, then the LM head fused with the top-1 and the standalone top-1 over its logits
+        nbytes = pvlc.top1_workspace_bytes()
+        tws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        pvlc.workspace_init(tws, nbytes, stream)
+        result = torch.zeros(2, dtype=torch.int32, device=dev)
         for _ in range(args.profile_steps):
             step(separate)
+            pvlc.lm_head_top1_f16(head_w, inputs[1024], logits, GEMV_HEAD[1], GEMV_HEAD[2], result, tws, nbytes,
+                                  stream)
+            pvlc.logits_top1_f32(logits, GEMV_HEAD[1], result, tws, nbytes, stream)
         torch.cuda.synchronize()
-        print(json.dumps({"profile_steps": args.profile_steps, "launches_per_step": len(separate)}))
+        print(json.dumps({"profile_steps": args.profile_steps, "launches_per_step": len(separate) + 2}))
         return 0
     for _ in range(args.warmup):
         step(separate)
@@ -460,6 +468,8 @@ def bench_gemv(args):
         t = _timed_launches(torch, stream, k, fn)
         shapes[f"{name} {rows}x{columns}"] = {"us": round(t * 1e3, 2),
                                               "gbps": round(gemv_bytes(rows, columns) / (t * 1e-3) / 1e9, 1)}
+        if name == GEMV_HEAD[0]:
+            top1 = _bench_top1(pvlc, torch, stream, ws, inputs[columns], out, rows, columns, k)
         del ws
     torch.cuda.synchronize()
 
@@ -478,11 +488,42 @@ def bench_gemv(args):
         "rows_concatenated": {"launches_per_step": len(fused), "us": round(ms_fused * 1e3, 2),
                               "gbps": round(gbps_fused, 1), "pct_hbm_peak": round(100 * gbps_fused / HBM_PEAK_GBPS, 2)},
         "per_shape_hbm": shapes,
+        "lm_head_top1": top1,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = gemv_cpu_baseline(separate, logits, args.cpu_seconds, step_bytes)
     print(json.dumps(result, ensure_ascii=False))
     return 0
+
+
+def _bench_top1(pvlc, torch, stream, heads, hidden, logits, rows, columns, k):
+    """Greedy selection after the LM head: the GEMV fused with the top-1 (one launch) against the GEMV followed
+    by the standalone top-1 over the logits (two launches), rotating over the same weight copies."""
+    nbytes = pvlc.top1_workspace_bytes()
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=logits.device)
+    pvlc.workspace_init(ws, nbytes, stream)
+    result = torch.zeros(2, dtype=torch.int32, device=logits.device)
+    n = len(heads)
+
+    def fused(i):
+        pvlc.lm_head_top1_f16(heads[i % n], hidden, logits, rows, columns, result, ws, nbytes, stream)
+
+    def two(i):
+        pvlc.gemv_f16(heads[i % n], hidden, logits, rows, columns, stream)
+        pvlc.logits_top1_f32(logits, rows, result, ws, nbytes, stream)
+
+    def alone(i):
+        pvlc.logits_top1_f32(logits, rows, result, ws, nbytes, stream)
+
+    for i in range(n):
+        fused(i)
+        two(i)
+    t_fused = _timed_launches(torch, stream, k, fused)
+    t_two = _timed_launches(torch, stream, k, two)
+    t_alone = _timed_launches(torch, stream, 200, alone)
+    return {"fused_us": round(t_fused * 1e3, 2), "gemv_then_top1_us": round(t_two * 1e3, 2),
+            "top1_alone_us": round(t_alone * 1e3, 2),
+            "fused_gbps": round(gemv_bytes(rows, columns) / (t_fused * 1e-3) / 1e9, 1)}
 
 
 def gemv_cpu_baseline(calls, logits, seconds, step_bytes):

@@ -420,6 +420,37 @@ pvlc_hip_status pvlc_hip_gemv_tiled_plan_create(uint32_t rows, uint32_t columns,
 pvlc_hip_status pvlc_hip_gemv_f16(const uint16_t *weights, const float *vector, float *out, uint32_t rows,
                                   uint32_t columns, void *stream);
 
+/* ---------------------------------------------------------------------------
+ * LM head and greedy top-1 on the device.
+ * ------------------------------------------------------------------------- */
+
+/* Bytes of the top-1 workspace (64 candidate slots, one per 256-byte line:
+ * 16384 bytes).  Zero it once (pvlc_hip_workspace_init); every call leaves it
+ * zeroed, so calls ordered on one stream reuse it; calls that overlap on one
+ * workspace race.  The pointer must be 256-byte aligned.  Each top-1 call is
+ * two launches on the caller's stream: the scan (or the LM-head GEMV), whose
+ * workgroups fold their best into the slots, and a one-wave finish that reads
+ * and clears them. */
+size_t pvlc_hip_top1_workspace_bytes(void);
+
+/* decoder_logits_top1_f32 (pvlc-runtime-web decoder_stack_session.rs:308-366,
+ * dispatched by top1_decoder_stack_session, web.rs:2628): result[0] = index of
+ * the largest of `vocab` f32 logits under the total order key
+ * bits ^ ((u32)(bits >> 31) >> 1) (-NaN < -inf < -0 < +0 < +inf < +NaN), equal
+ * keys to the lowest index; result[1] = that logit's f32 bits.  Device
+ * pointers, caller stream; 1 <= vocab <= 2^31. */
+pvlc_hip_status pvlc_hip_logits_top1_f32(const float *logits, uint32_t vocab, uint32_t *result, void *workspace,
+                                         size_t workspace_bytes, void *stream);
+
+/* The LM-head GEMV (pvlc_hip_gemv_f16 semantics and admission: the logits
+ * pass of decoder_stack_session.rs, gemv_tiled_f16_weights at 103424 x 1024)
+ * and the top-1 above over its output, selected while the GEMV streams (no
+ * second pass over the logits).  logits may be NULL
+ * (not written); result as pvlc_hip_logits_top1_f32 over the same logits. */
+pvlc_hip_status pvlc_hip_lm_head_top1_f16(const uint16_t *weights, const float *hidden, float *logits, uint32_t rows,
+                                          uint32_t columns, uint32_t *result, void *workspace, size_t workspace_bytes,
+                                          void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,7 @@ def _declare(l: ctypes.CDLL) -> None:
     l.oracle_causal_gqa_f32.argtypes = [_F, _SZ, _F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, _SZ, _F]
     l.oracle_append_kv_f32.argtypes = [_F, _F, _SZ, _F, _SZ, _F, _SZ, _SZ, _SZ, _F, _F]
     l.oracle_linear_f32.argtypes = [_F, _SZ, _SZ, _SZ, _F, _SZ, _F, _SZ, _SZ, _F]
+    l.oracle_top1_f32.argtypes = [_F, _SZ, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32)]
     l.oracle_write_prefill_kv_f32.argtypes = [_F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, _F, _F]
     l.oracle_rope_neox_f32.argtypes = [_F, _SZ, _SZ, _SZ, _SZ, _U32, _SZ, ctypes.c_float]
     l.oracle_mrope_f32.argtypes = [_F, _SZ, _F, _SZ, _SZ, _SZ, _SZ, _SZ, _F, _F, _SZ,
@@ -118,6 +119,14 @@ def causal_gqa_f32(query, key, value, tokens, query_heads, key_value_heads, head
     _check(lib().oracle_causal_gqa_f32(_ptr(q, _F), q.size, _ptr(k, _F), k.size, _ptr(v, _F), v.size,
                                        tokens, query_heads, key_value_heads, head_dim, _ptr(out, _F)))
     return out[: q.size]
+
+
+def top1_f32(logits) -> tuple[int, int]:
+    """decoder_logits_top1_f32 (decoder_stack_session.rs:308-366): (index, f32 bits of the logit)."""
+    x = _f32(logits).ravel()
+    index, bits = ctypes.c_uint32(), ctypes.c_uint32()
+    _check(lib().oracle_top1_f32(_ptr(x, _F), x.size, ctypes.byref(index), ctypes.byref(bits)))
+    return index.value, bits.value
 
 
 def linear_f32(input, rows, input_width, weights, bias, output_width) -> np.ndarray:

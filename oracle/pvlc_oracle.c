@@ -216,6 +216,34 @@ int oracle_linear_f32(const float *input, size_t input_len, size_t rows, size_t 
     return ORACLE_OK;
 }
 
+/* decoder_stack_session.rs:318-321: signed-integer key of an f32 that orders
+ * -NaN < -inf < ... < -0 < +0 < ... < +inf < +NaN. */
+static int32_t total_order_key(float value) {
+    int32_t bits;
+    memcpy(&bits, &value, sizeof bits);
+    return bits ^ (int32_t)((uint32_t)(bits >> 31) >> 1);
+}
+
+int oracle_top1_f32(const float *logits, size_t n, uint32_t *index, uint32_t *value_bits) {
+    if (n == 0) return ORACLE_DIMENSION_MISMATCH;
+    /* :323-328, :339-346: a candidate replaces the best on a larger key, or an
+     * equal key at a lower index; a scan in index order keeps the first of the
+     * equal keys, which is the order-independent answer of the tree reduction
+     * (:352-366). */
+    size_t best = 0;
+    int32_t best_key = total_order_key(logits[0]);
+    for (size_t i = 1; i < n; ++i) {
+        int32_t key = total_order_key(logits[i]);
+        if (key > best_key) {
+            best_key = key;
+            best = i;
+        }
+    }
+    *index = (uint32_t)best;
+    memcpy(value_bits, &logits[best], sizeof *value_bits);
+    return ORACLE_OK;
+}
+
 int oracle_write_prefill_kv_f32(const float *rotated_key, size_t key_len, const float *value,
                                 size_t value_len, size_t tokens, size_t key_value_heads, size_t head_dim,
                                 float *out_keys, float *out_values) {

@@ -27,6 +27,9 @@
  *   oracle_linear_f32       the reference's known answer (vision_contract.rs:433-441),
  *                           its error cases (:444-470), exact small-integer
  *                           products against numpy, an f64 bound.
+ *   oracle_top1_f32         an independent numeric comparator (value, sign of
+ *                           zero, lowest index) on finite logits, brute force;
+ *                           NaN/inf/signed-zero orderings worked by hand.
  */
 #ifndef PVLC_ORACLE_H
 #define PVLC_ORACLE_H
@@ -66,6 +69,13 @@ int oracle_causal_gqa_f32(const float *query, size_t query_len, const float *key
 int oracle_linear_f32(const float *input, size_t input_len, size_t rows, size_t input_width,
                       const float *weights, size_t weights_len, const float *bias, size_t bias_len,
                       size_t output_width, float *out);
+
+/* decoder_logits_top1_f32 (pvlc-runtime-web decoder_stack_session.rs:308-366)
+ * and its host twin top1FromLogitsBytes (web/engine/greedy_generation.mjs:43-79)
+ * without the host's finite check: the index of the largest logit under the
+ * f32 total order key bits ^ ((u32)(bits >> 31) >> 1), ties to the lowest
+ * index; value_bits = the f32 bits of that logit.  n = 0 is a dimension error. */
+int oracle_top1_f32(const float *logits, size_t n, uint32_t *index, uint32_t *value_bits);
 
 /* append_decoder_kv_cache, lib.rs:1420-1450: out = prefix rows || one new row. */
 int oracle_append_kv_f32(const float *prefix_keys, const float *prefix_values, size_t prefix_tokens,

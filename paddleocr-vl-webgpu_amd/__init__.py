@@ -190,6 +190,9 @@ SIGNATURES = {
     "pvlc_hip_kv_unpack_f16": ([_VP, _VP, _U32, _VP, _U32, _VP, _VP, _VP], ctypes.c_int32),
     "pvlc_hip_gemv_tiled_plan_create": ([_U32, _U32, ctypes.POINTER(GemvTiledPlanC)], ctypes.c_int32),
     "pvlc_hip_gemv_f16": ([_VP, _VP, _VP, _U32, _U32, _VP], ctypes.c_int32),
+    "pvlc_hip_top1_workspace_bytes": ([], _SZ),
+    "pvlc_hip_logits_top1_f32": ([_VP, _U32, _VP, _VP, _SZ, _VP], ctypes.c_int32),
+    "pvlc_hip_lm_head_top1_f16": ([_VP, _VP, _VP, _U32, _U32, _VP, _VP, _SZ, _VP], ctypes.c_int32),
 }
 
 
@@ -372,6 +375,25 @@ def gemv_f16(weights, vector, out, rows: int, columns: int, stream=None) -> None
     """out[r] = sum_c weights[r][c] * vector[c] (fp16 weights, f32 vector and output): replaces
     gemv_tiled_f16_weights (pvlc-wgsl lib.rs:1770-1835); admission as plan_gemv_tiled."""
     _check(lib.pvlc_hip_gemv_f16(_ptr(weights), _ptr(vector), _ptr(out), rows, columns, _stream(stream)))
+
+
+def top1_workspace_bytes() -> int:
+    """Bytes of the top-1 workspace (arrival counter + candidate slots); zero it once with workspace_init."""
+    return int(lib.pvlc_hip_top1_workspace_bytes())
+
+
+def logits_top1_f32(logits, vocab: int, result, workspace, workspace_bytes: int, stream=None) -> None:
+    """decoder_logits_top1_f32 (decoder_stack_session.rs:308-366): result[0] = index of the largest logit
+    under the f32 total order (ties to the lowest index), result[1] = its f32 bits."""
+    _check(lib.pvlc_hip_logits_top1_f32(_ptr(logits), vocab, _ptr(result), _ptr(workspace), workspace_bytes,
+                                        _stream(stream)))
+
+
+def lm_head_top1_f16(weights, hidden, logits, rows: int, columns: int, result, workspace, workspace_bytes: int,
+                     stream=None) -> None:
+    """LM-head GEMV (gemv_f16 semantics) and the top-1 of its logits in one launch; logits may be None."""
+    _check(lib.pvlc_hip_lm_head_top1_f16(_ptr(weights), _ptr(hidden), _ptr(logits), rows, columns, _ptr(result),
+                                         _ptr(workspace), workspace_bytes, _stream(stream)))
 
 
 def plan_prefill(tokens: int, cache_capacity: int) -> None:

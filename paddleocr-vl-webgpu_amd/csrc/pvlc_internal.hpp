@@ -100,6 +100,19 @@ int launch_prefill(const pvlc_hip_paged_prefill_args *args, void *stream);
 int launch_gemv_f16(const uint16_t *weights, const float *vector, float *out, uint32_t rows, uint32_t columns,
                     void *stream);
 
+// Top-1 workspace: kTop1Slots slots of 256 bytes, each a packed u64
+// candidate; zero before the first launch, zero again after each launch.
+constexpr uint32_t kTop1Slots = 64;
+struct Top1Slot {
+    uint64_t best;
+    uint64_t pad[31];
+};
+static_assert(sizeof(Top1Slot) == 256, "one slot per 256-byte line");
+constexpr size_t kTop1WorkspaceBytes = kTop1Slots * sizeof(Top1Slot);
+int launch_gemv_top1_f16(const uint16_t *weights, const float *vector, float *logits, uint32_t rows,
+                         uint32_t columns, Top1Slot *slots, uint32_t *result, void *stream);
+int launch_logits_top1_f32(const float *logits, uint32_t vocab, Top1Slot *slots, uint32_t *result, void *stream);
+
 // GemvTiledDescriptor::plan (runtime-core lib.rs:753-785); returns a status.
 int plan_gemv_tiled(uint32_t rows, uint32_t columns, pvlc_hip_gemv_tiled_plan *out);
 

@@ -486,6 +486,47 @@ pvlc_hip_status pvlc_hip_gemv_f16(const uint16_t *weights, const float *vector, 
     return ok();
 }
 
+size_t pvlc_hip_top1_workspace_bytes(void) { return kTop1WorkspaceBytes; }
+
+namespace {
+pvlc_hip_status top1_workspace(void *workspace, size_t workspace_bytes, uint32_t *result, Top1Slot **slots) {
+    if (!workspace || !result) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "top-1 workspace or result pointer is NULL");
+    if (workspace_bytes < kTop1WorkspaceBytes)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "top-1 workspace holds " + std::to_string(workspace_bytes) +
+                                                         " bytes but needs " + std::to_string(kTop1WorkspaceBytes));
+    if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "top-1 workspace must be 256-byte aligned");
+    *slots = static_cast<Top1Slot *>(workspace);
+    return PVLC_HIP_OK;
+}
+}  // namespace
+
+pvlc_hip_status pvlc_hip_logits_top1_f32(const float *logits, uint32_t vocab, uint32_t *result, void *workspace,
+                                         size_t workspace_bytes, void *stream) {
+    if (!logits) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "logits pointer is NULL");
+    if (vocab == 0 || vocab > 0x80000000u)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "top-1 needs 1 <= vocab <= 2^31 logits");
+    if (reinterpret_cast<uintptr_t>(logits) % 4 != 0)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "logits must be 4-byte aligned f32");
+    Top1Slot *slots = nullptr;
+    if (pvlc_hip_status st = top1_workspace(workspace, workspace_bytes, result, &slots)) return st;
+    const int e = launch_logits_top1_f32(logits, vocab, slots, result, stream);
+    if (e != 0) return hip_fail(static_cast<hipError_t>(e), "top-1 launch");
+    return ok();
+}
+
+pvlc_hip_status pvlc_hip_lm_head_top1_f16(const uint16_t *weights, const float *hidden, float *logits, uint32_t rows,
+                                          uint32_t columns, uint32_t *result, void *workspace, size_t workspace_bytes,
+                                          void *stream) {
+    if (!weights || !hidden) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "LM-head buffer pointer is NULL");
+    if (pvlc_hip_status st = plan_gemv_tiled(rows, columns, nullptr)) return st;
+    Top1Slot *slots = nullptr;
+    if (pvlc_hip_status st = top1_workspace(workspace, workspace_bytes, result, &slots)) return st;
+    const int e = launch_gemv_top1_f16(weights, hidden, logits, rows, columns, slots, result, stream);
+    if (e != 0) return hip_fail(static_cast<hipError_t>(e), "LM-head top-1 launch");
+    return ok();
+}
+
 size_t pvlc_hip_paged_decode_workspace_bytes(uint32_t num_seqs, uint32_t max_context, uint32_t partition_tokens) {
     if (num_seqs == 0 || max_context == 0) return 0;
     if (partition_tokens == 0) return decode_workspace_layout(num_seqs, auto_workspace_parts(num_seqs, max_context)).total;

@@ -97,3 +97,36 @@ def test_dot_bound_of_the_gemv_parity_test_catches_planted_mistakes():
     assert dot_error_ratio(O.linear_f32(x, 1, columns, shifted, zero, rows), wf, x, columns // 64 + 6) > 10
     square = wf[:, :rows].T.copy()
     assert dot_error_ratio(O.linear_f32(x[:rows], 1, rows, square, zero, rows), wf[:, :rows], x[:rows], 6) > 10
+
+
+def test_top1_workspace_is_a_fixed_small_block():
+    assert pvlc.top1_workspace_bytes() == 64 * 256
+
+
+def test_device_top1_entry_points_validate_before_touching_the_gpu():
+    nbytes = pvlc.top1_workspace_bytes()
+    aligned = 1 << 20  # a fake 256-byte aligned device address: never dereferenced on these paths
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.logits_top1_f32(aligned, 0, aligned, aligned, nbytes)
+    assert code(e.value) == ("InvalidInvocation", "LengthMismatch")
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.logits_top1_f32(aligned, 2**31 + 1, aligned, aligned, nbytes)
+    assert code(e.value) == ("InvalidInvocation", "LengthMismatch")
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.logits_top1_f32(aligned, 100, aligned, aligned, nbytes - 8)
+    assert code(e.value) == ("InvalidInvocation", "LengthMismatch")
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.logits_top1_f32(aligned, 100, aligned, aligned + 8, nbytes)
+    assert code(e.value) == ("InvalidInvocation", "LengthMismatch")
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.logits_top1_f32(aligned, 100, None, aligned, nbytes)
+    assert code(e.value) == ("InvalidInvocation", "LengthMismatch")
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.lm_head_top1_f16(aligned, aligned, None, 103_424, 4096, aligned, aligned, nbytes)
+    assert code(e.value) == ("InvalidInvocation", "InvalidDecoderGeometry")
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.lm_head_top1_f16(aligned, aligned, None, 0, 1024, aligned, aligned, nbytes)
+    assert code(e.value) == ("InvalidInvocation", "InvalidDecoderGeometry")
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.lm_head_top1_f16(aligned, aligned, None, 103_424, 1024, aligned, None, nbytes)
+    assert code(e.value) == ("InvalidInvocation", "LengthMismatch")

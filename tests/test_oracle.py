@@ -408,3 +408,53 @@ def test_linear_is_exact_on_small_integers_and_within_f64_bound():
     assert np.all(np.abs(out - exact) <= bound)
     # a dropped term or a transposed weight layout would not pass
     assert np.max(np.abs(out - (w.reshape(2048, 64).astype(np.float64).T @ x))) > 1.0
+
+
+# ---------------------------------------------------------------------------
+# top-1 over logits (decoder_stack_session.rs:308-366, greedy_generation.mjs:43-79)
+# ---------------------------------------------------------------------------
+
+def _f32_bits(x):
+    return int(np.array([x], np.float32).view(np.uint32)[0])
+
+
+def _numeric_top1(values):
+    """Independent comparator for non-NaN logits: larger value, then +0 over -0, then the lower index."""
+    import math
+    return max(range(len(values)), key=lambda i: (float(values[i]), math.copysign(1.0, float(values[i])), -i))
+
+
+def test_top1_matches_a_numeric_comparator_on_random_logits_with_ties():
+    rng = np.random.default_rng(31)
+    for n in (1, 2, 3, 17, 256, 1000, 4099):
+        for trial in range(4):
+            x = rng.standard_normal(n).astype(np.float32)
+            if trial >= 1:  # planted ties of the maximum (and quantised values)
+                x = np.round(x * 4) / 4
+            if trial == 3 and n > 2:
+                x[rng.integers(0, n, 3)] = x.max()
+            idx, bits = O.top1_f32(x)
+            want = _numeric_top1(x)
+            assert idx == want and bits == _f32_bits(x[want]), (n, trial)
+
+
+def test_top1_total_order_on_special_values():
+    nan, neg_nan = np.float32(np.nan), -np.float32(np.nan)
+    inf = np.float32(np.inf)
+    cases = [
+        ([-0.0, 0.0], 1), ([0.0, -0.0], 0), ([-0.0, -0.0], 0),
+        ([1.0, nan, inf], 1), ([inf, nan], 1), ([neg_nan, -inf], 1), ([neg_nan], 0),
+        ([-inf, -inf, -inf], 0), ([-3.0, -1e-45, -1.0], 1), ([1e-45, 0.0, -0.0], 0),
+        ([5.0, 7.0, 7.0, 6.0], 1), ([np.float32(3.4028235e38), inf, inf], 1),
+    ]
+    for values, want in cases:
+        x = np.array(values, np.float32)
+        idx, bits = O.top1_f32(x)
+        assert idx == want, (values, idx)
+        assert bits == int(x.view(np.uint32)[want])
+
+
+def test_top1_rejects_an_empty_logit_row():
+    with pytest.raises(O.OracleError) as e:
+        O.top1_f32(np.zeros(0, np.float32))
+    assert e.value.code == "DimensionMismatch"
