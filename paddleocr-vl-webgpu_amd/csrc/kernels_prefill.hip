@@ -1,8 +1,8 @@
 // Causal prefill for gfx950: rotary + range append into the paged cache, then
 // MFMA flash attention over the cache.
 //
-// Kernel 1 (4 tokens per workgroup): rotates the 2 key heads and writes them
-// with the values into the blocked cache (the same rounding as the decode
+// Kernel 1 (one 16-token cache block per workgroup): rotates the 2 key heads
+// and writes them with the values into the blocked cache (the same rounding as the decode
 // append, so prefill and decode leave bit-identical rows), and, when the
 // caller passes a query scratch, writes the rotated queries there.  Replaces
 // decoder_prefill_mrope_f32 and decoder_kv_append_range_f32
@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "pvlc_device.hpp"
 #include "pvlc_internal.hpp"
@@ -71,56 +72,97 @@ __device__ inline uint32_t cache_block(const PrefillParams &p, uint32_t tile, bo
     return *ok ? static_cast<uint32_t>(b) : 0u;
 }
 
-// Kernel 1: 4 tokens per workgroup, 64 threads per token: threads 0-31
-// rotate the token's 2 key heads (8 dims each) and write them into the
-// cache, threads 32-63 scatter its values.  With a query scratch the
+// Kernel 1: one workgroup per 16-token cache block, both key heads.  Every
+// thread rotates two 8-dim key chunks (item = head, chunk, token; 16
+// consecutive threads fill one 256-byte run of the key slab) and writes one
+// 32-byte value row of the slab (head, dim: 16 tokens) after a transpose of
+// the block's value rows through LDS, so every cache store is a full 16-byte
+// vector and each 32-byte sector is written once.  With a query scratch the
 // workgroup also writes the rotated queries of its tokens (the attention
-// kernel rotates its own query fragments, so the scratch is only an output
-// for callers that want it).
-constexpr int kAppendTokens = 4;
+// kernel rotates its own query fragments, so the scratch is only an output for
+// callers that want it).
+constexpr int kAppendThreads = 256;
 
-__global__ __launch_bounds__(256) void prefill_rope_append_kernel(PrefillParams p) {
+// Rotary position of token t and whether its tables hold it (bit 4 of the
+// error word otherwise, reported once per token by the caller's choice).
+__device__ inline int rope_position(const PrefillParams &p, uint32_t t, bool *rope) {
+    const int pos = p.positions ? p.positions[t] : static_cast<int>(t);
+    *rope = p.rope_cos != nullptr && pos >= 0 && static_cast<uint32_t>(pos) < p.rope_rows;
+    return pos;
+}
+
+__global__ __launch_bounds__(kAppendThreads) void prefill_rope_append_kernel(PrefillParams p) {
     const int i = threadIdx.x;
-    const uint32_t t = blockIdx.x * kAppendTokens + (i >> 6);
-    const int sub = i & 63;
-    if (t < p.tokens) {
-        bool rope = p.rope_cos != nullptr;
-        const int pos = p.positions ? p.positions[t] : static_cast<int>(t);
-        if (rope && (pos < 0 || static_cast<uint32_t>(pos) >= p.rope_rows)) {
-            if (sub == 0 && p.error_word) atomicOr(p.error_word, 4u);
-            rope = false;
-        }
-        const float *cos_row = rope ? p.rope_cos + static_cast<size_t>(pos) * 64 : nullptr;
-        const float *sin_row = rope ? p.rope_sin + static_cast<size_t>(pos) * 64 : nullptr;
-        bool ok;
-        const uint32_t blk = cache_block(p, t / kBlockTokens, &ok);
-        if (!ok) {
-            if (sub == 0 && p.error_word) atomicOr(p.error_word, 2u);
-        } else {
-            const int hh = (sub >> 4) & 1, c = sub & 15, d0 = c * 8;
-            const size_t slab = (static_cast<size_t>(blk) * kKvHeads + hh) * kBlockHeadElems;
-            const uint32_t tt = t % kBlockTokens;
-            if (sub < 32) {
-                const uint16_t *krow = p.key + (static_cast<size_t>(t) * kKvHeads + hh) * kHeadDim;
-                const half8_t k = rope ? rotate_chunk(krow, d0, cos_row, sin_row)
-                                       : *reinterpret_cast<const half8_t *>(krow + d0);
-                *reinterpret_cast<half8_t *>(p.key_cache + slab + c * 128 + key_slot(static_cast<int>(tt)) * 8) = k;
-            } else {
-                const u16x8_t v = *reinterpret_cast<const u16x8_t *>(
-                    p.value + (static_cast<size_t>(t) * kKvHeads + hh) * kHeadDim + d0);
+    const uint32_t b = blockIdx.x;  // cache block (16 tokens) of the sequence
+    const uint32_t t0 = b * kBlockTokens;
+    const uint32_t ntok = min(p.tokens - t0, kBlockTokens);
+    __shared__ uint16_t sv[kBlockTokens][kRowElems + 8];  // value rows, padded against bank conflicts
+
+    // value rows of the block: 16 tokens x 256 fp16, two 16-byte pieces per
+    // thread, loaded now and staged into LDS after the key loads are issued
+    u16x8_t vrow[2];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) p.value_cache[slab + (d0 + j) * kBlockTokens + tt] = v[j];
+    for (int r = 0; r < 2; ++r) {
+        const int k = i + r * kAppendThreads;
+        const uint32_t t = t0 + min(static_cast<uint32_t>(k >> 5), ntok - 1);
+        vrow[r] = *reinterpret_cast<const u16x8_t *>(p.value + static_cast<size_t>(t) * kRowElems + (k & 31) * 8);
+    }
+
+    bool ok;
+    const uint32_t blk = cache_block(p, b, &ok);
+    if (!ok && i == 0 && p.error_word) atomicOr(p.error_word, 2u);
+    // keys: item (head, chunk, token), 16 consecutive threads per 256-byte run
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int k = i + r * kAppendThreads;
+        const int tt = k & 15, c = (k >> 4) & 15, hh = k >> 8;
+        if (static_cast<uint32_t>(tt) < ntok) {
+            const uint32_t t = t0 + tt;
+            bool rope;
+            const int pos = rope_position(p, t, &rope);
+            if (!rope && p.rope_cos != nullptr && c == 0 && hh == 0 && p.error_word) atomicOr(p.error_word, 4u);
+            const uint16_t *krow = p.key + (static_cast<size_t>(t) * kKvHeads + hh) * kHeadDim;
+            const half8_t kv = rope ? rotate_chunk(krow, c * 8, p.rope_cos + static_cast<size_t>(pos) * 64,
+                                                   p.rope_sin + static_cast<size_t>(pos) * 64)
+                                    : *reinterpret_cast<const half8_t *>(krow + c * 8);
+            const size_t slab = (static_cast<size_t>(blk) * kKvHeads + hh) * kBlockHeadElems;
+            if (ok) *reinterpret_cast<half8_t *>(p.key_cache + slab + c * 128 + key_slot(tt) * 8) = kv;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int k = i + r * kAppendThreads;
+        *reinterpret_cast<u16x8_t *>(&sv[k >> 5][(k & 31) * 8]) = vrow[r];
+    }
+    __syncthreads();
+    if (ok) {
+        // value slab row (head, dim): the block's 16 tokens; a partial last
+        // block keeps the slab's other tokens as they were
+        const int hh = i >> 7, d = i & 127;
+        const size_t slab = (static_cast<size_t>(blk) * kKvHeads + hh) * kBlockHeadElems;
+        uint16_t *dst = p.value_cache + slab + d * kBlockTokens;
+        if (ntok == kBlockTokens) {
+            u16x8_t lo, hi;
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) {
+                lo[tt] = sv[tt][hh * kHeadDim + d];
+                hi[tt] = sv[tt + 8][hh * kHeadDim + d];
             }
+            *reinterpret_cast<u16x8_t *>(dst) = lo;
+            *reinterpret_cast<u16x8_t *>(dst + 8) = hi;
+        } else {
+            for (uint32_t tt = 0; tt < ntok; ++tt) dst[tt] = sv[tt][hh * kHeadDim + d];
         }
     }
     if (p.qrot) {
-        // (token, head, 8-dim chunk) items of the workgroup's tokens.
-        for (int k = i; k < kAppendTokens * kQueryHeads * 16; k += 256) {
-            const uint32_t tq = blockIdx.x * kAppendTokens + k / (kQueryHeads * 16);
-            if (tq >= p.tokens) break;
+        // (token, head, 8-dim chunk) items of the block's tokens
+        for (int k = i; k < static_cast<int>(kBlockTokens * kQueryHeads * 16); k += kAppendThreads) {
+            const int tt = k / (kQueryHeads * 16);
+            if (static_cast<uint32_t>(tt) >= ntok) break;
+            const uint32_t tq = t0 + tt;
             const int h = (k >> 4) % kQueryHeads, d0 = (k & 15) * 8;
-            const int pos = p.positions ? p.positions[tq] : static_cast<int>(tq);
-            const bool rope = p.rope_cos != nullptr && pos >= 0 && static_cast<uint32_t>(pos) < p.rope_rows;
+            bool rope;
+            const int pos = rope_position(p, tq, &rope);
             const uint16_t *qrow = p.query + (static_cast<size_t>(tq) * kQueryHeads + h) * kHeadDim;
             const half8_t q = rope ? rotate_chunk(qrow, d0, p.rope_cos + static_cast<size_t>(pos) * 64,
                                                   p.rope_sin + static_cast<size_t>(pos) * 64)
@@ -216,44 +258,49 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     const int steps = (nkeys + kKeyStep - 1) / kKeyStep;
     const int last_tile = (nkeys - 1) >> 4;
 
-    // Double-buffered LDS; each thread moves 4 key and 4 value chunks of 16
-    // bytes per step through registers (loaded one step ahead).
-    __shared__ uint16_t sk[2][kStepElems];
-    __shared__ uint16_t sv[2][kStepElems];
-    u16x8_t pk[4], pv[4];
-    int koff[4], voff[4];
-    {
-        const int c = static_cast<int>(threadIdx.x);  // chunk of a tile: keys chunk*16 + slot, values dim*2 + half
-        const int kchunk = c >> 4, kslot = c & 15;
-        const int vdim = c >> 1, vhalf = c & 1;
+    // Double-buffered LDS, filled by direct global-to-LDS loads (16 bytes a
+    // lane: lane l of a wave's load lands at the wave's LDS base + 16 l).
+    // Each wave issues 4 key and 4 value loads per step; lane and load index
+    // pick the global chunk that belongs at that LDS position of the layouts
+    // above.  Steps past the end re-read the last tile (never used).
+    // Four distinct arrays (not one indexed by parity): the main loop picks
+    // them at compile time, so the compiler sees that a step's loads into LDS
+    // and its LDS reads touch different buffers and does not wait for the
+    // loads before the reads.
+    __shared__ uint16_t sk0[kStepElems], sk1[kStepElems];
+    __shared__ uint16_t sv0[kStepElems], sv1[kStepElems];
+    typedef __attribute__((address_space(3))) void *lds_ptr;
+    auto dma_k = [&](int step, uint16_t *dst) {
+        // LDS chunk q = 64 k + lane (k = 4 wave + r): slot8 = lane & 7,
+        // tile = lane bit 3, h = lane bit 4, dim-chunk = 2 (k & 7) + lane bit 5, pair j = k >> 3
+        const int j = wave >> 1;
+        bool ok;
+        const uint32_t b0 = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + 2 * j, last_tile)), &ok);
+        const uint32_t b1 = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + 2 * j + 1, last_tile)), &ok);
+        const uint32_t blk = (lane & 8) ? b1 : b0;
+        const uint16_t *src = p.key_cache + (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems +
+                              (((lane >> 4) & 1) * 8 + (lane & 7)) * 8 + (lane >> 5) * 128;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {  // tile i of the step
-            koff[i] = lds_key_offset(i >> 1, kchunk, kslot >> 3, i & 1, kslot & 7);
-            voff[i] = lds_value_offset(i >> 1, i & 1, vhalf, vdim);
-        }
-    }
-    // Thread t moves 16-byte chunk t of each of the step's 4 tiles (the
-    // tile index is uniform, so the block-table read is a scalar load).
-    auto gload = [&](int step) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            bool ok;
-            const uint32_t blk = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + i, last_tile)), &ok);
-            const size_t slab = (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems;
-            pk[i] = *reinterpret_cast<const u16x8_t *>(p.key_cache + slab + threadIdx.x * 8);
-            pv[i] = *reinterpret_cast<const u16x8_t *>(p.value_cache + slab + threadIdx.x * 8);
+        for (int r = 0; r < 4; ++r) {
+            const int k = 4 * wave + r;
+            __builtin_amdgcn_global_load_lds(src + (2 * (k & 7)) * 128, (lds_ptr)(dst + 64 * k * 8), 16, 0, 0);
         }
     };
-    auto lstore = [&](int buf) {
+    auto dma_v = [&](int step, uint16_t *dst) {
+        // LDS chunk q = 64 k + lane: dim = (k & 1) 64 + lane, half = (k >> 1) & 1,
+        // tile = (k >> 2) & 1 = wave & 1, pair j = k >> 3 = wave >> 1
+        bool ok;
+        const uint32_t blk = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + wave, last_tile)), &ok);
+        const uint16_t *src = p.value_cache + (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems + lane * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *reinterpret_cast<u16x8_t *>(&sk[buf][koff[i]]) = pk[i];
-            *reinterpret_cast<u16x8_t *>(&sv[buf][voff[i]]) = pv[i];
+        for (int r = 0; r < 4; ++r) {
+            const int k = 4 * wave + r;
+            __builtin_amdgcn_global_load_lds(src + (r & 1) * 64 * 16 + (r >> 1) * 8, (lds_ptr)(dst + 64 * k * 8), 16,
+                                             0, 0);
         }
     };
 
-    float m_run[2] = {-INFINITY, -INFINITY};  // raw (unscaled) running max of this lane's column
-    float4_t o[2][9];                          // 8 column tiles of the output, then the row sums
+    float4_t o[2][9];  // 8 column tiles of the output, then the row sums
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
@@ -263,18 +310,10 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     for (int e = 0; e < 8; ++e) ones[e] = static_cast<_Float16>(1.0f);
     const float scale = p.scale_log2;
 
-    gload(0);
-    lstore(0);
-    if (steps > 1) gload(1);
-    __syncthreads();
-    for (int step = 0; step < steps; ++step) {
-        const int buf = step & 1;
-        const uint16_t *kl = sk[buf];
-        const uint16_t *vl = sv[buf];
-        const int kbase = step * kKeyStep;
-        // Scores: MFMA h of pair j leaves lane (column = query token, kg) the
-        // keys (kg & 1)*8 + h*4 + r of the pair's tile kg >> 1.
-        float x[2][2][8];
+    // Scores of one step: MFMA h of pair j leaves lane (column = query token,
+    // kg) the keys (kg & 1)*8 + h*4 + r of the pair's tile kg >> 1.
+    typedef float Scores[2][2][8];
+    auto scores = [&](const uint16_t *kl, Scores &x) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -293,68 +332,140 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
 #pragma unroll
                     for (int r = 0; r < 4; ++r) x[ct][j][h * 4 + r] = acc[ct][r];
             }
-        // The causal mask and the end of the sequence only touch steps that
-        // reach past the first query token of the block.
-        if (kbase + kKeyStep - 1 > t0 || kbase + kKeyStep > n) {  // uniform
+    };
+    // The causal mask and the end of the sequence only touch steps that
+    // reach past the first query token of the block.
+    auto needs_mask = [&](int step) { return step * kKeyStep + kKeyStep - 1 > t0 || step * kKeyStep + kKeyStep > n; };
+    auto apply_mask = [&](int step, Scores &x) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int key = kbase + (2 * j + (kg >> 1)) * 16 + (kg & 1) * 8 + e;
-                    const bool keep = key <= my_token && key < n;
+            for (int e = 0; e < 8; ++e) {
+                const int key = step * kKeyStep + (2 * j + (kg >> 1)) * 16 + (kg & 1) * 8 + e;
+                const bool keep = key <= my_token && key < n;
 #pragma unroll
-                    for (int ct = 0; ct < 2; ++ct) x[ct][j][e] = keep ? x[ct][j][e] : -INFINITY;
-                }
-        }
-        half8_t pa[2][2];
+                for (int ct = 0; ct < 2; ++ct) x[ct][j][e] = keep ? x[ct][j][e] : -INFINITY;
+            }
+    };
+    // Running max of the column (the 4 lanes of a column hold its 64 keys).
+    auto column_max = [&](const Scores &x, const float (&m)[2], float (&m_new)[2]) {
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
-            float cmax = -INFINITY;
+            float c = m[ct];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) cmax = fmaxf(cmax, x[ct][j][e]);
-            cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-            cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-            // Step 0 always holds key 0 <= every query token, so m_new is finite.
-            const float m_new = fmaxf(m_run[ct], cmax);
-            const float ms = m_new * scale;
-            if (__any(m_new != m_run[ct]) && step > 0) {
-                const float alpha = __builtin_amdgcn_exp2f(m_run[ct] * scale - ms);
+                for (int e = 0; e < 8; ++e) c = fmaxf(c, x[ct][j][e]);
+            c = fmaxf(c, __shfl_xor(c, 16));
+            m_new[ct] = fmaxf(c, __shfl_xor(c, 32));
+        }
+    };
+    // P of pair j in fp16 (the A operand of P.V), log2 units, scale folded in.
+    auto probs = [&](const Scores &x, const float (&ms)[2], int j, half8_t (&pa)[2][2]) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pa[ct][j][e] = to_h(__builtin_amdgcn_exp2f(__builtin_fmaf(x[ct][j][e], scale, -ms[ct])));
+    };
+    // O += P.V over pair j, and the row sums += P.1 (exactly the rounded weights).
+    auto pv_mfma = [&](const uint16_t *vl, int j, const half8_t (&pa)[2][2]) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const half8_t vf = *reinterpret_cast<const half8_t *>(vl + lds_value_offset(j, kg >> 1, kg & 1, c * 16 + row));
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) o[ct][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ct][j], vf, o[ct][c], 0, 0, 0);
+        }
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) o[ct][8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ct][j], ones, o[ct][8], 0, 0, 0);
+    };
+
+    // Software pipeline: while the score MFMAs of step i+1 run, the VALU
+    // rescales O and exponentiates half of step i; while P.V of step i runs,
+    // it exponentiates the other half, then masks step i+1 and takes its max.
+    // K stays one step ahead of V through LDS: step i (parity i & 1) reads
+    // K(i+1) from sk[(i+1)&1] and V(i) from sv[i&1], and at its start loads
+    // K(i+2) into sk[i&1] and V(i+1) into sv[(i+1)&1] (both freed by step
+    // i-1), waited for at its closing barrier.
+    dma_k(0, sk0);
+    dma_v(0, sv0);
+    dma_k(1, sk1);
+    __syncthreads();
+    Scores xa, xb;
+    float m_run[2], ms[2], alpha[2] = {1.f, 1.f};
+    bool rescale = false;
+    {
+        scores(sk0, xa);
+        if (needs_mask(0)) apply_mask(0, xa);  // uniform
+        const float minus_inf[2] = {-INFINITY, -INFINITY};
+        column_max(xa, minus_inf, m_run);  // finite: key 0 <= every query token
+    }
+    __syncthreads();  // every wave has read sk[0] before step 0 stores K(2) there
+
+    // Step i.  more: a step i+1 exists (its scores are computed here);
+    // mask_next: step i+1 is the last step, the only one that reaches the
+    // diagonal or the end of the sequence (query blocks are 16-aligned inside
+    // 64-key steps), so the mask stays out of the main loop.  K(i+2) exists
+    // exactly when more && !mask_next.  The main loop passes compile-time
+    // flags (one straight-line region, buffers known at compile time); the
+    // last steps pass runtime flags.
+    auto step_body = [&](auto more, auto mask_next, auto odd, int i, Scores &xc, Scores &xn) {
+        uint16_t *k_read = odd ? sk0 : sk1;  // K(i+1)
+        uint16_t *k_load = odd ? sk1 : sk0;  // K(i+2)
+        uint16_t *v_read = odd ? sv1 : sv0;  // V(i)
+        uint16_t *v_load = odd ? sv0 : sv1;  // V(i+1)
+        if (rescale) {  // uniform: some column's max moved in step i
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float a = __shfl(alpha, kg * 4 + r);
+                    const float a = __shfl(alpha[ct], kg * 4 + r);
 #pragma unroll
                     for (int c = 0; c < 9; ++c) o[ct][c][r] *= a;
                 }
+        }
+        if (more && !mask_next) dma_k(i + 2, k_load);
+        if (more) dma_v(i + 1, v_load);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) ms[ct] = m_run[ct] * scale;
+        half8_t pa[2][2];
+        // scores of step i+1 | P of step i, pair 0
+        if (more) scores(k_read, xn);
+        probs(xc, ms, 0, pa);
+        // P.V of pair 0 | P of pair 1
+        pv_mfma(v_read, 0, pa);
+        probs(xc, ms, 1, pa);
+        // P.V of pair 1 | mask and max of step i+1
+        pv_mfma(v_read, 1, pa);
+        if (more) {
+            if (mask_next) apply_mask(i + 1, xn);
+            float m_new[2];
+            column_max(xn, m_run, m_new);
+            bool moved = false;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                alpha[ct] = __builtin_amdgcn_exp2f((m_run[ct] - m_new[ct]) * scale);
+                moved |= m_new[ct] != m_run[ct];
+                m_run[ct] = m_new[ct];
             }
-            m_run[ct] = m_new;
+            rescale = __any(moved);
+        }
+        __syncthreads();  // waits for this wave's loads into LDS, then for every wave
+    };
+    const std::integral_constant<bool, true> yes;
+    const std::integral_constant<bool, false> no;
+    int i = 0;
+    for (; i + 3 < steps; i += 2) {
+        step_body(yes, no, no, i, xa, xb);
+        step_body(yes, no, yes, i + 1, xb, xa);
+    }
+    for (; i < steps; ++i) {  // the last one to three steps
+        step_body(i + 1 < steps, i + 2 == steps, (i & 1) != 0, i, xa, xb);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    pa[ct][j][e] = to_h(__builtin_amdgcn_exp2f(__builtin_fmaf(x[ct][j][e], scale, -ms)));
-        }
-        // P.V, and P.1 for the row sums (exactly the rounded weights P.V uses).
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const half8_t vf = *reinterpret_cast<const half8_t *>(
-                    vl + lds_value_offset(j, kg >> 1, kg & 1, c * 16 + row));
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct)
-                    o[ct][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ct][j], vf, o[ct][c], 0, 0, 0);
-            }
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
-                o[ct][8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ct][j], ones, o[ct][8], 0, 0, 0);
-        }
-        if (step + 1 < steps) {
-            lstore(buf ^ 1);  // its last readers finished before the previous barrier
-            if (step + 2 < steps) gload(step + 2);
-        }
-        __syncthreads();
+                for (int e = 0; e < 8; ++e) xa[ct][j][e] = xb[ct][j][e];
     }
 
     // Normalise: output row kg*4 + r of tile ct is query token t0 + kg*4 + r;
@@ -396,8 +507,8 @@ int launch_prefill(const pvlc_hip_paged_prefill_args *a, void *stream) {
     p.error_word = a->error_word;
     p.scale_log2 = kLog2e / sqrtf(static_cast<float>(kHeadDim));
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(prefill_rope_append_kernel, dim3((a->tokens + kAppendTokens - 1) / kAppendTokens), dim3(256), 0,
-                       st, p);
+    hipLaunchKernelGGL(prefill_rope_append_kernel, dim3((a->tokens + kBlockTokens - 1) / kBlockTokens),
+                       dim3(kAppendThreads), 0, st, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     const unsigned qblocks = (a->tokens + kQueryBlock - 1) / kQueryBlock;
