@@ -369,7 +369,14 @@ typedef struct pvlc_hip_paged_prefill_args {
     const int32_t *positions; /* [N] or NULL = 0..N-1 */
     uint16_t *query_scratch;  /* optional [N][16][128] fp16: receives the rotated query (NULL: not written) */
     uint32_t *error_word;     /* optional: bit 1 = block id out of range (row skipped), bit 2 = position outside the rope table */
+    void *workspace;          /* optional, 256-byte aligned, zeroed once (pvlc_hip_workspace_init): split-K schedule
+                                 (long query blocks split over several workgroups and merged); NULL: one workgroup
+                                 per query block.  Launches that share one workspace must be stream-ordered. */
+    uint64_t workspace_bytes; /* at least pvlc_hip_paged_prefill_workspace_bytes(tokens) when workspace is given */
 } pvlc_hip_paged_prefill_args;
+
+/* Bytes of the split-K prefill workspace for N tokens (0: nothing splits). */
+size_t pvlc_hip_paged_prefill_workspace_bytes(uint32_t tokens);
 
 /* Causal prefill: rotary on Q and K, write all N K/V rows into the blocked
  * cache, then MFMA causal GQA attention (fp16 in, f32 accumulate, fp16 out).

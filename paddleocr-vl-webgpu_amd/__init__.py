@@ -149,7 +149,7 @@ class PagedPrefillArgsC(ctypes.Structure):
     _fields_ = [("tokens", _U32), ("num_blocks", _U32), ("block_table", _VP), ("key_cache", _VP),
                 ("value_cache", _VP), ("query", _VP), ("key", _VP), ("value", _VP), ("out", _VP),
                 ("rope_cos", _VP), ("rope_sin", _VP), ("rope_rows", _U32), ("positions", _VP),
-                ("query_scratch", _VP), ("error_word", _VP)]
+                ("query_scratch", _VP), ("error_word", _VP), ("workspace", _VP), ("workspace_bytes", ctypes.c_uint64)]
 
 
 # Exported symbols with their C signatures (argtypes, restype).
@@ -191,6 +191,7 @@ SIGNATURES = {
     "pvlc_hip_gemv_tiled_plan_create": ([_U32, _U32, ctypes.POINTER(GemvTiledPlanC)], ctypes.c_int32),
     "pvlc_hip_gemv_f16": ([_VP, _VP, _VP, _U32, _U32, _VP], ctypes.c_int32),
     "pvlc_hip_top1_workspace_bytes": ([], _SZ),
+    "pvlc_hip_paged_prefill_workspace_bytes": ([_U32], _SZ),
     "pvlc_hip_logits_top1_f32": ([_VP, _U32, _VP, _VP, _SZ, _VP], ctypes.c_int32),
     "pvlc_hip_lm_head_top1_f16": ([_VP, _VP, _VP, _U32, _U32, _VP, _VP, _SZ, _VP], ctypes.c_int32),
 }
@@ -581,14 +582,20 @@ def paged_decode_f16(args: PagedDecodeArgsC, stream=None) -> None:
     _check(lib.pvlc_hip_paged_decode_f16(ctypes.byref(args), _stream(stream)))
 
 
+def prefill_workspace_bytes(tokens: int) -> int:
+    """Bytes of the split-K prefill workspace (0 when no query block splits)."""
+    return int(lib.pvlc_hip_paged_prefill_workspace_bytes(tokens))
+
+
 def paged_prefill_f16(*, tokens, num_blocks, key_cache, value_cache, query, key, value, out, query_scratch=None,
                       block_table=None, rope_cos=None, rope_sin=None, rope_rows=0, positions=None,
-                      error_word=None, stream=None) -> None:
+                      error_word=None, workspace=None, workspace_bytes=0, stream=None) -> None:
     """Causal prefill with rotary and paged range append
-    (replaces decoder_prefill_mrope/kv_append_range/prefill_gqa, wgsl lib.rs:1262-1416)."""
+    (replaces decoder_prefill_mrope/kv_append_range/prefill_gqa, wgsl lib.rs:1262-1416); with a workspace the
+    long query blocks are split over several workgroups and merged (split-K)."""
     a = PagedPrefillArgsC(tokens, num_blocks, _ptr(block_table), _ptr(key_cache), _ptr(value_cache), _ptr(query),
                           _ptr(key), _ptr(value), _ptr(out), _ptr(rope_cos), _ptr(rope_sin), rope_rows,
-                          _ptr(positions), _ptr(query_scratch), _ptr(error_word))
+                          _ptr(positions), _ptr(query_scratch), _ptr(error_word), _ptr(workspace), workspace_bytes)
     _check(lib.pvlc_hip_paged_prefill_f16(ctypes.byref(a), _stream(stream)))
 
 

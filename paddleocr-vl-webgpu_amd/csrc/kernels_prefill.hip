@@ -60,6 +60,10 @@ struct PrefillParams {
     uint16_t *qrot;
     uint32_t *error_word;
     float scale_log2;
+    // split-K pair schedule (a workspace was given and the blocks are long)
+    bool split;
+    uint32_t *counters;  // [pair][kv head]
+    float *partials;     // [pair][kv head][2 parts][kPrefillPartialFloats]
 };
 
 __device__ inline uint32_t cache_block(const PrefillParams &p, uint32_t tile, bool *ok) {
@@ -202,12 +206,32 @@ __device__ inline void prefill_item(int b, int qblocks, int *qb, uint32_t *g) {
 __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(PrefillParams p) {
     const int n = static_cast<int>(p.tokens);
     const int qblocks = (n + kQueryBlock - 1) / kQueryBlock;
-    int qb;
-    uint32_t g;
-    prefill_item(static_cast<int>(blockIdx.x), qblocks, &qb, &g);
+    uint32_t g, pair = 0;
+    PrefillSegment seg0{}, seg1{};
+    int nseg = 1;
+    if (p.split) {
+        nseg = static_cast<int>(prefill_pair_segments(blockIdx.x, static_cast<uint32_t>(qblocks), &g, &pair, &seg0, &seg1));
+    } else {
+        int qb0;
+        prefill_item(static_cast<int>(blockIdx.x), qblocks, &qb0, &g);
+        seg0 = {static_cast<uint32_t>(qb0), 0u, 1u, 0u, prefill_block_steps(static_cast<uint32_t>(qb0))};
+    }
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int row = lane & 15, kg = lane >> 4;
+    // Four distinct arrays (not one indexed by parity): the main loop picks
+    // them at compile time, so the compiler sees that a step's loads into LDS
+    // and its LDS reads touch different buffers and does not wait for the
+    // loads before the reads.
+    __shared__ uint16_t sk0[kStepElems], sk1[kStepElems];
+    __shared__ uint16_t sv0[kStepElems], sv1[kStepElems];
+    __shared__ bool sm_last;
+
+  // One segment: a whole query block, or one part of a split one.
+  auto run_segment = [&](const PrefillSegment sg) {
+    const int qb = static_cast<int>(sg.qb);
+    const uint32_t part = sg.part, nparts = sg.nparts;
+    const int s_begin = static_cast<int>(sg.step_begin), steps = static_cast<int>(sg.steps);
     const int t0 = qb * kQueryBlock;
     const int my_token = t0 + row;  // query token of this lane's column
 
@@ -255,20 +279,14 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     }
 
     const int nkeys = min(t0 + kQueryBlock, n);
-    const int steps = (nkeys + kKeyStep - 1) / kKeyStep;
     const int last_tile = (nkeys - 1) >> 4;
+    const bool last_part = part + 1 == nparts;
 
     // Double-buffered LDS, filled by direct global-to-LDS loads (16 bytes a
     // lane: lane l of a wave's load lands at the wave's LDS base + 16 l).
     // Each wave issues 4 key and 4 value loads per step; lane and load index
     // pick the global chunk that belongs at that LDS position of the layouts
     // above.  Steps past the end re-read the last tile (never used).
-    // Four distinct arrays (not one indexed by parity): the main loop picks
-    // them at compile time, so the compiler sees that a step's loads into LDS
-    // and its LDS reads touch different buffers and does not wait for the
-    // loads before the reads.
-    __shared__ uint16_t sk0[kStepElems], sk1[kStepElems];
-    __shared__ uint16_t sv0[kStepElems], sv1[kStepElems];
     typedef __attribute__((address_space(3))) void *lds_ptr;
     auto dma_k = [&](int step, uint16_t *dst) {
         // LDS chunk q = 64 k + lane (k = 4 wave + r): slot8 = lane & 7,
@@ -386,26 +404,27 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     // K(i+1) from sk[(i+1)&1] and V(i) from sv[i&1], and at its start loads
     // K(i+2) into sk[i&1] and V(i+1) into sv[(i+1)&1] (both freed by step
     // i-1), waited for at its closing barrier.
-    dma_k(0, sk0);
-    dma_v(0, sv0);
-    dma_k(1, sk1);
+    dma_k(s_begin, sk0);
+    dma_v(s_begin, sv0);
+    dma_k(s_begin + 1, sk1);
     __syncthreads();
     Scores xa, xb;
     float m_run[2], ms[2], alpha[2] = {1.f, 1.f};
     bool rescale = false;
     {
         scores(sk0, xa);
-        if (needs_mask(0)) apply_mask(0, xa);  // uniform
+        if (needs_mask(s_begin)) apply_mask(s_begin, xa);  // uniform: only the block's last step
         const float minus_inf[2] = {-INFINITY, -INFINITY};
         column_max(xa, minus_inf, m_run);  // finite: key 0 <= every query token
     }
     __syncthreads();  // every wave has read sk[0] before step 0 stores K(2) there
 
-    // Step i.  more: a step i+1 exists (its scores are computed here);
-    // mask_next: step i+1 is the last step, the only one that reaches the
-    // diagonal or the end of the sequence (query blocks are 16-aligned inside
-    // 64-key steps), so the mask stays out of the main loop.  K(i+2) exists
-    // exactly when more && !mask_next.  The main loop passes compile-time
+    // Step i of the unit (block step s_begin + i).  more: a step i+1 exists
+    // (its scores are computed here); mask_next: step i+1 is the block's last
+    // step, the only one that reaches the diagonal or the end of the sequence
+    // (query blocks are 16-aligned inside 64-key steps), so the mask stays out
+    // of the main loop.  K(i+2) is loaded when more && !mask_next (a unit that
+    // is not the block's last part loads one step past its end, never read).  The main loop passes compile-time
     // flags (one straight-line region, buffers known at compile time); the
     // last steps pass runtime flags.
     auto step_body = [&](auto more, auto mask_next, auto odd, int i, Scores &xc, Scores &xn) {
@@ -423,8 +442,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
                     for (int c = 0; c < 9; ++c) o[ct][c][r] *= a;
                 }
         }
-        if (more && !mask_next) dma_k(i + 2, k_load);
-        if (more) dma_v(i + 1, v_load);
+        if (more && !mask_next) dma_k(s_begin + i + 2, k_load);
+        if (more) dma_v(s_begin + i + 1, v_load);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) ms[ct] = m_run[ct] * scale;
         half8_t pa[2][2];
@@ -437,7 +456,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
         // P.V of pair 1 | mask and max of step i+1
         pv_mfma(v_read, 1, pa);
         if (more) {
-            if (mask_next) apply_mask(i + 1, xn);
+            if (mask_next) apply_mask(s_begin + i + 1, xn);
             float m_new[2];
             column_max(xn, m_run, m_new);
             bool moved = false;
@@ -459,13 +478,83 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
         step_body(yes, no, yes, i + 1, xb, xa);
     }
     for (; i < steps; ++i) {  // the last one to three steps
-        step_body(i + 1 < steps, i + 2 == steps, (i & 1) != 0, i, xa, xb);
+        step_body(i + 1 < steps, i + 2 == steps && last_part, (i & 1) != 0, i, xa, xb);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) xa[ct][j][e] = xb[ct][j][e];
+    }
+
+    if (nparts > 1) {
+        // Split block: store this part's (m, O, l), count it, and let the part
+        // that arrives last merge the other one.  Partials move as 8-byte
+        // relaxed agent-scope atomics (coherent across the XCDs' L2s); every
+        // store of the workgroup completes before thread 0 counts the arrival.
+        // Slab of a part: O/l tiles [wave][ct][tile][half][lane] as float
+        // pairs, then m [wave][ct][lane].
+        const uint32_t item = pair * kKvHeads + g;  // the heavy block of the pair
+        auto slab = [&](uint32_t q) {
+            return reinterpret_cast<uint64_t *>(p.partials + (static_cast<size_t>(item) * 2 + q) * kPrefillPartialFloats);
+        };
+        auto pair_idx = [&](int ct, int c, int hf) { return (((wave * 2 + ct) * 9 + c) * 2 + hf) * 64 + lane; };
+        auto m_ptr = [&](uint32_t q, int ct) {
+            return p.partials + (static_cast<size_t>(item) * 2 + q) * kPrefillPartialFloats + 4 * 2 * 9 * 4 * 64 +
+                   (wave * 2 + ct) * 64 + lane;
+        };
+        {
+            uint64_t *own = slab(part);
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+#pragma unroll
+                for (int c = 0; c < 9; ++c)
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf) {
+                        const uint64_t bits = static_cast<uint64_t>(__float_as_uint(o[ct][c][2 * hf])) |
+                                              (static_cast<uint64_t>(__float_as_uint(o[ct][c][2 * hf + 1])) << 32);
+                        __hip_atomic_store(own + pair_idx(ct, c, hf), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                __hip_atomic_store(m_ptr(part, ct), m_run[ct], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const uint32_t prev =
+                __hip_atomic_fetch_add(p.counters + item, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sm_last = prev == nparts - 1;
+        }
+        __syncthreads();
+        if (!sm_last) return;  // uniform: the other part merges and writes the block
+        const uint32_t q = part ^ 1u;  // two parts
+        const uint64_t *other = slab(q);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const float mo = __hip_atomic_load(m_ptr(q, ct), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            float4_t ov[9];
+#pragma unroll
+            for (int c = 0; c < 9; ++c)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const uint64_t bits = __hip_atomic_load(other + pair_idx(ct, c, hf), __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT);
+                    ov[c][2 * hf] = __uint_as_float(static_cast<uint32_t>(bits));
+                    ov[c][2 * hf + 1] = __uint_as_float(static_cast<uint32_t>(bits >> 32));
+                }
+            const float m_new = fmaxf(m_run[ct], mo);
+            const float a_self = __builtin_amdgcn_exp2f((m_run[ct] - m_new) * scale);
+            const float a_other = __builtin_amdgcn_exp2f((mo - m_new) * scale);
+            m_run[ct] = m_new;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float as = __shfl(a_self, kg * 4 + r);
+                const float ao = __shfl(a_other, kg * 4 + r);
+#pragma unroll
+                for (int c = 0; c < 9; ++c) o[ct][c][r] = o[ct][c][r] * as + ov[c][r] * ao;
+            }
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(p.counters + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // Normalise: output row kg*4 + r of tile ct is query token t0 + kg*4 + r;
@@ -484,6 +573,11 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
             }
         }
     }
+  };
+  // a light block, then part of a heavy one (two inlined copies: each is
+  // register-allocated like a single segment)
+  if (nseg > 0) run_segment(seg0);
+  if (nseg > 1) run_segment(seg1);
 }
 
 }  // namespace
@@ -512,7 +606,14 @@ int launch_prefill(const pvlc_hip_paged_prefill_args *a, void *stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     const unsigned qblocks = (a->tokens + kQueryBlock - 1) / kQueryBlock;
-    hipLaunchKernelGGL(prefill_attention_kernel, dim3(qblocks * kKvHeads), dim3(kWaves * 64), 0, st, p);
+    const PrefillWorkspace ws = prefill_workspace_layout(a->tokens);
+    p.split = a->workspace != nullptr && ws.total > 0;
+    if (p.split) {
+        p.counters = static_cast<uint32_t *>(a->workspace);
+        p.partials = reinterpret_cast<float *>(static_cast<unsigned char *>(a->workspace) + ws.partial_offset);
+    }
+    const unsigned grid = p.split ? prefill_pair_workgroups(qblocks) : qblocks * kKvHeads;
+    hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(kWaves * 64), 0, st, p);
     return static_cast<int>(hipGetLastError());
 }
 

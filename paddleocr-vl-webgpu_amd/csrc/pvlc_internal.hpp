@@ -97,6 +97,62 @@ int launch_kv_pack(const uint16_t *key_rows, const uint16_t *value_rows, uint32_
 int launch_kv_unpack(const uint16_t *key_cache, const uint16_t *value_cache, uint32_t tokens, const int32_t *table,
                      uint32_t num_blocks, uint16_t *key_rows, uint16_t *value_rows, void *stream);
 int launch_prefill(const pvlc_hip_paged_prefill_args *args, void *stream);
+
+// Split-K pair schedule of the causal prefill.  Query block qb (16 tokens)
+// of one kv head attends qb/4 + 1 steps of 64 keys, so a grid of one
+// workgroup per block is as long as its last block while most compute units
+// idle.  With a workspace, block l and block qblocks-1-l of a kv head (about
+// qblocks/4 + 2 steps together) go to two workgroups of equal length: the
+// first runs the light block, then the first k steps of the heavy one; the
+// second runs the rest of the heavy block (which holds the diagonal), and the
+// one that finishes last merges the two parts.  Used when the longest block
+// is longer than kPrefillSplitSteps.
+constexpr uint32_t kPrefillSplitSteps = 32;
+constexpr uint32_t kPrefillPartialFloats = 4 * 64 * 74;  // 4 waves x 64 lanes x (2 x 9 x 4 O/l + 2 m)
+
+constexpr uint32_t prefill_block_steps(uint32_t qb) { return qb / 4 + 1; }
+constexpr uint32_t prefill_max_steps(uint32_t qblocks) { return (qblocks - 1) / 4 + 1; }
+constexpr uint32_t prefill_pairs(uint32_t qblocks) { return (qblocks + 1) / 2; }
+constexpr uint32_t prefill_pair_workgroups(uint32_t qblocks) { return 4u * prefill_pairs(qblocks); }
+
+struct PrefillSegment {
+    uint32_t qb, part, nparts, step_begin, steps;
+};
+
+// Segments of workgroup w of the pair grid (w = (pair * 2 + g) * 2 + role);
+// returns their number (0..2).
+constexpr uint32_t prefill_pair_segments(uint32_t w, uint32_t qblocks, uint32_t *g, uint32_t *pair,
+                                         PrefillSegment *first, PrefillSegment *second) {
+    const uint32_t role = w & 1u, pg = w >> 1;
+    *g = pg & 1u;
+    *pair = pg >> 1;
+    const uint32_t heavy = qblocks - 1u - *pair, light = *pair;
+    const uint32_t sh = prefill_block_steps(heavy), sl = light == heavy ? 0u : prefill_block_steps(light);
+    const uint32_t k = (sh - sl + 1u) / 2u;  // heavy steps the light block's workgroup takes
+    PrefillSegment *out[2] = {first, second};
+    uint32_t n = 0;
+    if (role == 0) {
+        if (sl) *out[n++] = {light, 0u, 1u, 0u, sl};
+        if (k >= sh) *out[n++] = {heavy, 0u, 1u, 0u, sh};
+        else if (k > 0) *out[n++] = {heavy, 0u, 2u, 0u, k};
+    } else {
+        if (k == 0) *out[n++] = {heavy, 0u, 1u, 0u, sh};
+        else if (k < sh) *out[n++] = {heavy, 1u, 2u, k, sh - k};
+    }
+    return n;
+}
+// Workspace of the pair schedule: an arrival counter per (pair, kv head),
+// then two partial slabs each; 0 when the blocks are short enough.
+struct PrefillWorkspace {
+    size_t partial_offset, total;
+};
+inline PrefillWorkspace prefill_workspace_layout(uint32_t tokens) {
+    const uint32_t qblocks = (tokens + 15u) / 16u;
+    if (tokens == 0 || prefill_max_steps(qblocks) <= kPrefillSplitSteps) return {0, 0};
+    const uint32_t items = 2u * prefill_pairs(qblocks);
+    const size_t counters = (static_cast<size_t>(items) * 4 + 255) / 256 * 256;
+    return {counters, counters + static_cast<size_t>(items) * 2 * kPrefillPartialFloats * 4};
+}
 int launch_gemv_f16(const uint16_t *weights, const float *vector, float *out, uint32_t rows, uint32_t columns,
                     void *stream);
 

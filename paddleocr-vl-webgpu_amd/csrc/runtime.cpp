@@ -586,6 +586,8 @@ pvlc_hip_status pvlc_hip_kv_unpack_f16(const uint16_t *key_cache, const uint16_t
     return ok();
 }
 
+size_t pvlc_hip_paged_prefill_workspace_bytes(uint32_t tokens) { return prefill_workspace_layout(tokens).total; }
+
 pvlc_hip_status pvlc_hip_paged_prefill_f16(const pvlc_hip_paged_prefill_args *args, void *stream) {
     if (!args) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill args are NULL");
     if (args->tokens == 0 || args->num_blocks == 0)
@@ -598,6 +600,16 @@ pvlc_hip_status pvlc_hip_paged_prefill_f16(const pvlc_hip_paged_prefill_args *ar
         return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION, "rotary table shorter than the prefill");
     if (!args->block_table && (args->tokens + kBlockTokens - 1) / kBlockTokens > args->num_blocks)
         return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "tokens exceed the contiguous blocks");
+    if (args->workspace) {
+        const PrefillWorkspace ws = prefill_workspace_layout(args->tokens);
+        if (args->workspace_bytes < ws.total)
+            return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill workspace holds " +
+                                                             std::to_string(args->workspace_bytes) +
+                                                             " bytes but the split schedule needs " +
+                                                             std::to_string(ws.total));
+        if (reinterpret_cast<uintptr_t>(args->workspace) % 256 != 0)
+            return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill workspace must be 256-byte aligned");
+    }
     const int e = launch_prefill(args, stream);
     if (e != 0) return hip_fail(static_cast<hipError_t>(e), "prefill launch");
     return ok();

@@ -16,7 +16,15 @@ pytestmark = pytest.mark.gpu
 BASE = 500000.0
 
 
-def run_prefill(n, seed, table=None, num_blocks=None, scale=0.5, rope=True, with_scratch=False):
+def prefill_workspace(n):
+    import torch
+    nbytes = pvlc.prefill_workspace_bytes(n)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device="cuda")
+    pvlc.workspace_init(ws, ws.numel())
+    return ws, nbytes
+
+
+def run_prefill(n, seed, table=None, num_blocks=None, scale=0.5, rope=True, with_scratch=False, workspace=None):
     import torch
     nb = num_blocks or (n + 15) // 16
     q = f16_bits(seed, n * 2048, scale)
@@ -33,7 +41,9 @@ def run_prefill(n, seed, table=None, num_blocks=None, scale=0.5, rope=True, with
     pvlc.paged_prefill_f16(tokens=n, num_blocks=nb, key_cache=d_k, value_cache=d_v, query=keep[0], key=keep[1],
                            value=keep[2], out=out, query_scratch=scratch, block_table=d_t,
                            rope_cos=keep[3] if rope else None, rope_sin=keep[4] if rope else None,
-                           rope_rows=n if rope else 0, error_word=err)
+                           rope_rows=n if rope else 0, error_word=err,
+                           workspace=workspace[0] if workspace else None,
+                           workspace_bytes=workspace[1] if workspace else 0)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
     tab = table if table is not None else np.arange(nb)
@@ -90,3 +100,36 @@ def test_prefill_config4_sampled_rows_at_4096():
     for i in (0, 1, 15, 16, 17, 255, 1000, 2047, 3333, 4095):
         want = O.decode_gqa_f32(qr[i * 2048:(i + 1) * 2048], kr[:(i + 1) * W], vr[:(i + 1) * W], i + 1, 16, 2, 128)
         check_close(out[i], want, f"config4 row {i}")
+
+
+def sampled_rows_match_decode(out, qr, kr, vr, n, rows, label):
+    out = out.reshape(n, 2048)
+    for i in rows:
+        want = O.decode_gqa_f32(qr[i * 2048:(i + 1) * 2048], kr[:(i + 1) * W], vr[:(i + 1) * W], i + 1, 16, 2, 128)
+        check_close(out[i], want, f"{label} row {i}")
+
+
+@pytest.mark.parametrize("n", [2049, 2100, 3000, 4096])
+def test_split_schedule_matches_the_oracle(n):
+    """Long query blocks split over two workgroups and merged by the last one to finish (a workspace is
+    given): rows on both sides of the split point and the last rows, against decode over i + 1 keys."""
+    log(f"case: split prefill N={n}")
+    ws = prefill_workspace(n)
+    assert ws[1] > 0
+    out, qr, kr, vr, scratch, q = run_prefill(n, seed=5000 + n, workspace=ws)
+    rows = sorted({0, 17, 2047, 2048, 2100 % n, n - 17, n - 2, n - 1} | {min(n - 1, 2048 + 64 * k) for k in (1, 7)})
+    sampled_rows_match_decode(out, qr, kr, vr, n, rows, f"split N={n}")
+
+
+def test_split_and_unsplit_schedules_agree_and_the_workspace_is_reusable():
+    import torch
+    n = 4096
+    ws = prefill_workspace(n)
+    plain = run_prefill(n, seed=42)[0]
+    first = run_prefill(n, seed=42, workspace=ws)[0]
+    second = run_prefill(n, seed=42, workspace=ws)[0]
+    np.testing.assert_array_equal(first, second)  # two parts merge in a fixed order: bit-identical
+    assert float(np.abs(first - plain).max()) <= 1e-3
+    # every arrival counter is back to zero
+    counters = ws[0][:256 * 2].view(torch.int32)
+    assert int(counters.abs().sum().item()) == 0

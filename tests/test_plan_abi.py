@@ -275,3 +275,28 @@ def test_runtime_without_gpu_reports_adapter_unavailable():
     with pytest.raises(pvlc.PvlcHipError) as e:
         pvlc.NativeRuntime(0)
     assert e.value.code == "AdapterUnavailable"
+
+
+def test_prefill_workspace_is_only_needed_for_long_blocks():
+    # up to 2048 tokens every query block attends at most 32 steps of 64 keys and runs whole; beyond, block l
+    # and block qblocks-1-l share two workgroups: a counter and two partial slabs of 75776 bytes per pair and
+    # kv head
+    for n in (1, 16, 1000, 2048):
+        assert pvlc.prefill_workspace_bytes(n) == 0, n
+    for n in (2049, 3000, 4096, 8192):
+        pairs = ((n + 15) // 16 + 1) // 2
+        counters = -(-(2 * pairs * 4) // 256) * 256
+        assert pvlc.prefill_workspace_bytes(n) == counters + 2 * pairs * 2 * 75776, n
+
+
+def test_prefill_rejects_a_short_or_misaligned_workspace():
+    need = pvlc.prefill_workspace_bytes(4096)
+    fake = 1 << 20  # never dereferenced: validation fails first
+    common = dict(tokens=4096, num_blocks=256, key_cache=fake, value_cache=fake, query=fake, key=fake, value=fake,
+                  out=fake)
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.paged_prefill_f16(**common, workspace=fake, workspace_bytes=need - 4)
+    assert e.value.invocation_code == "LengthMismatch"
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.paged_prefill_f16(**common, workspace=fake + 4, workspace_bytes=need)
+    assert e.value.invocation_code == "LengthMismatch"
