@@ -332,24 +332,39 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     // kg) the keys (kg & 1)*8 + h*4 + r of the pair's tile kg >> 1.
     typedef float Scores[2][2][8];
     auto scores = [&](const uint16_t *kl, Scores &x) {
+        // 8 independent accumulator chains (pair j, slot half h, head ct), the
+        // 32-dim chunk kb outermost, so no MFMA waits on the previous one
+        float4_t acc[2][2][2];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                float4_t acc[2] = {float4_t{0.f, 0.f, 0.f, 0.f}, float4_t{0.f, 0.f, 0.f, 0.f}};
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                    const half8_t kf = *reinterpret_cast<const half8_t *>(
-                        kl + lds_key_offset(j, kb * 4 + kg, h, row >> 3, row & 7));
+                for (int ct = 0; ct < 2; ++ct) acc[j][h][ct] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            half8_t kf[2][2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    kf[j][h] = *reinterpret_cast<const half8_t *>(kl + lds_key_offset(j, kb * 4 + kg, h, row >> 3, row & 7));
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
 #pragma unroll
                     for (int ct = 0; ct < 2; ++ct)
-                        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ct][kb], acc[ct], 0, 0, 0);
-                }
+                        acc[j][h][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[j][h], qf[ct][kb], acc[j][h][ct], 0, 0, 0);
+        }
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct)
+        for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) x[ct][j][h * 4 + r] = acc[ct][r];
-            }
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) x[ct][j][h * 4 + r] = acc[j][h][ct][r];
     };
     // The causal mask and the end of the sequence only touch steps that
     // reach past the first query token of the block.
@@ -450,11 +465,17 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
         // scores of step i+1 | P of step i, pair 0
         if (more) scores(k_read, xn);
         probs(xc, ms, 0, pa);
-        // P.V of pair 0 | P of pair 1
+        // P.V of pair 0 | P of pair 1.  The P.V MFMAs run at raised wave
+        // priority, so the SIMD's other wave fills the gaps with its VALU work
+        // (measured 4-6% faster than equal priorities).
+        __builtin_amdgcn_s_setprio(1);
         pv_mfma(v_read, 0, pa);
+        __builtin_amdgcn_s_setprio(0);
         probs(xc, ms, 1, pa);
         // P.V of pair 1 | mask and max of step i+1
+        __builtin_amdgcn_s_setprio(1);
         pv_mfma(v_read, 1, pa);
+        __builtin_amdgcn_s_setprio(0);
         if (more) {
             if (mask_next) apply_mask(s_begin + i + 1, xn);
             float m_new[2];
