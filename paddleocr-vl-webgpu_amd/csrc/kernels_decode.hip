@@ -436,15 +436,20 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
     // workgroup completes (s_waitcnt vmcnt(0), then the barrier) before thread
     // 0 counts the arrival, which orders the partials before the count.
     // (A C++ release/acquire fence at agent scope would instead write back and
-    // invalidate the whole L2 of the XCD in every workgroup.)
+    // invalidate the whole L2 of the XCD in every workgroup.)  Values move in
+    // 8-byte pairs: half the transactions of single floats.
+    static_assert(kPer % 2 == 0, "partials move as float pairs");
+    auto pack = [](float lo, float hi) {
+        return static_cast<uint64_t>(__float_as_uint(lo)) | (static_cast<uint64_t>(__float_as_uint(hi)) << 32);
+    };
     if (active) {
 #pragma unroll
-        for (int e = 0; e < kPer; ++e)
-            __hip_atomic_store(part_o + e0 + e, po[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (d0 == 0) {
-            __hip_atomic_store(part_ml + 2 * h, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(part_ml + 2 * h + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        for (int e = 0; e < kPer; e += 2)
+            __hip_atomic_store(reinterpret_cast<uint64_t *>(part_o + e0 + e), pack(po[e], po[e + 1]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        if (d0 == 0)
+            __hip_atomic_store(reinterpret_cast<uint64_t *>(part_ml + 2 * h), pack(M, L), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
     // Wait for this wave's partial stores to complete (a single-wave
     // workgroup's __syncthreads() emits no wait), then for every wave.
@@ -463,7 +468,12 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
     // partitions at a time, and folds them into a running LSE combination.
     const float *all_o = p.part_o + unit * (kGroup * kHeadDim);
     const float *all_ml = p.part_ml + unit * (2 * kGroup);
-    auto ld = [](const float *q) { return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    auto ld2 = [](const float *q, float *lo, float *hi) {
+        const uint64_t v =
+            __hip_atomic_load(reinterpret_cast<const uint64_t *>(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *lo = __uint_as_float(static_cast<uint32_t>(v));
+        *hi = __uint_as_float(static_cast<uint32_t>(v >> 32));
+    };
     constexpr int kBatch = 8;
     float Mg = -INFINITY, Lg = 0.f, og[kPer];
 #pragma unroll
@@ -473,10 +483,10 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) {
             const int q = min(q0 + b, num_parts - 1);  // clamped re-reads get weight 0 below
-            mv[b] = ld(all_ml + q * (2 * kGroup) + 2 * h);
-            lv[b] = ld(all_ml + q * (2 * kGroup) + 2 * h + 1);
+            ld2(all_ml + q * (2 * kGroup) + 2 * h, &mv[b], &lv[b]);
 #pragma unroll
-            for (int e = 0; e < kPer; ++e) ov[b][e] = ld(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + e0 + e);
+            for (int e = 0; e < kPer; e += 2)
+                ld2(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + e0 + e, &ov[b][e], &ov[b][e + 1]);
         }
         float Mb = Mg;
 #pragma unroll
