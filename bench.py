@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                     help="2 = headline 18-layer step (default); 3 = paged ragged batch; 4 = causal prefill; "
                          "5 = long-context split-K batch")
+    ap.add_argument("--projection", action="store_true",
+                    help="prefill projections of one decoder layer at N=4096 (fp16 weights, f32 activations)")
     ap.add_argument("--gemv", action="store_true",
                     help="decoder weight GEMVs of one token step (18 layers x 7 projections + LM head, fp16 weights)")
     return ap.parse_args()
@@ -79,6 +81,8 @@ def main() -> int:
         return calibrate_copy(args)
     if args.gemv:
         return bench_gemv(args)
+    if args.projection:
+        return bench_projection(args)
     if args.config == 4:
         return bench_prefill(args)
     if args.config in (3, 5):
@@ -529,6 +533,69 @@ def _bench_top1(pvlc, torch, stream, heads, hidden, logits, rows, columns, k):
     return {"fused_us": round(t_fused * 1e3, 2), "gemv_then_top1_us": round(t_two * 1e3, 2),
             "top1_alone_us": round(t_alone * 1e3, 2),
             "fused_gbps": round(gemv_bytes(rows, columns) / (t_fused * 1e-3) / 1e9, 1)}
+
+
+# Prefill projections of one decoder layer, (name, output width, input width); q|k|v and gate|up as one
+# weight matrix each (rows concatenated), as the projection stages of the prefill plan consume them
+# (runtime-core lib.rs:2545-2560).
+PROJECTIONS = (("q|k|v", 2560, 1024), ("o", 1024, 2048), ("gate|up", 6144, 1024), ("down", 1024, 3072))
+
+
+def bench_projection(args):
+    """Prefill projections of one layer at N=4096 tokens: out = x . W^T + b with f32 activations and fp16
+    weights, each product W.(hi + lo) on MFMA (two fp16 MFMAs per product)."""
+    import torch
+
+    from __graft_entry__ import load_package
+
+    pvlc = load_package()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device=dev).manual_seed(12)
+    n = 4096
+    calls = []
+    for name, out_w, in_w in PROJECTIONS:
+        x = torch.randn(n * in_w, generator=gen, device=dev)
+        w = (torch.randn(out_w * in_w, generator=gen, device=dev) * 0.02).half()
+        b = torch.randn(out_w, generator=gen, device=dev)
+        y = torch.empty(n * out_w, device=dev)
+        wsb = pvlc.linear_projection_workspace_bytes(n, in_w)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        calls.append((name, out_w, in_w, x, w, b, y, ws, wsb))
+
+    def run(c):
+        name, out_w, in_w, x, w, b, y, ws, wsb = c
+        pvlc.linear_projection_f16(x, w, b, y, n, in_w, out_w, ws, wsb, stream)
+
+    if args.profile_steps:
+        for _ in range(args.profile_steps):
+            for c in calls:
+                run(c)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_steps": args.profile_steps}))
+        return 0
+    per = {}
+    total_flops, total_ms = 0, 0.0
+    for c in calls:
+        for _ in range(max(args.warmup, 5)):
+            run(c)
+        ms = _timed_launches(torch, stream, min(args.steps, 50), lambda i: run(c))
+        flops = 2 * n * c[1] * c[2]
+        per[f"{c[0]} {n}x{c[2]}->{c[1]}"] = {"us": round(ms * 1e3, 2), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+        total_flops += flops
+        total_ms += ms
+    tflops = total_flops / (total_ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "prefill projections of one decoder layer µs + TFLOP/s (N=4096, fp16 weights, f32 activations)",
+        "value": round(total_ms * 1e3, 2), "unit": "µs/layer", "steps": min(args.steps, 50), "warmup": args.warmup,
+        "dtype": "f16 weights, f32 activations split into fp16 hi+lo, f32 accumulate",
+        "config": {"workload": "N=4096: q|k|v 2560x1024, o 1024x2048, gate|up 6144x1024, down 1024x3072, + bias"},
+        "achieved_tflops": round(tflops, 1), "per_projection": per,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(tflops / 2500.0, 4),
+                     "note": "algorithmic FLOPs (2*N*out*in); the device issues two fp16 MFMAs per product, so "
+                             "1250 TFLOP/s is its own ceiling"}}, ensure_ascii=False))
+    return 0
 
 
 def gemv_cpu_baseline(calls, logits, seconds, step_bytes):

@@ -458,6 +458,62 @@ pvlc_hip_status pvlc_hip_lm_head_top1_f16(const uint16_t *weights, const float *
                                           uint32_t columns, uint32_t *result, void *workspace, size_t workspace_bytes,
                                           void *stream);
 
+/* ---------------------------------------------------------------------------
+ * Prefill projections with fp16 weights (multi-token linear layers).
+ * ------------------------------------------------------------------------- */
+
+/* VisionPatchProjectionBytesErrorCode, runtime-core lib.rs:1751-1759. */
+typedef enum pvlc_hip_projection_error {
+    PVLC_HIP_PROJ_OK = 0,
+    PVLC_HIP_PROJ_INVALID_GEOMETRY = 1,
+    PVLC_HIP_PROJ_OVERFLOW = 2,
+    PVLC_HIP_PROJ_LENGTH_MISMATCH = 3,
+    PVLC_HIP_PROJ_NON_FINITE = 4,
+    PVLC_HIP_PROJ_MISSING_SHADER_F16 = 5,
+    PVLC_HIP_PROJ_DISPATCH_LIMIT_EXCEEDED = 6
+} pvlc_hip_projection_error;
+
+/* VisionPatchProjectionBytesPlan, runtime-core lib.rs:1741-1749. */
+typedef struct pvlc_hip_projection_plan {
+    uint32_t kernel;         /* 0 = vision_patch_projection_f32, 1 = linear_projection_f16_weights */
+    uint32_t weight_storage; /* 0 = f32 weights, 1 = f16 weights */
+    uint64_t input_bytes;
+    uint64_t weight_bytes;
+    uint64_t bias_bytes;
+    uint64_t output_bytes;
+    uint32_t dispatch[3];
+} pvlc_hip_projection_plan;
+
+/* VisionPatchProjectionBytesDescriptor::plan (runtime-core lib.rs:1768-1840):
+ * positive geometry, widths a multiple of 4 for f16 weights, checked sizes,
+ * dispatch [ceil(out / 32), ceil(rows / 32), 1].  Returns the error code. */
+int32_t pvlc_hip_projection_plan_create(uint32_t patch_count, uint32_t input_width, uint32_t output_width,
+                                        uint32_t weight_storage, pvlc_hip_projection_plan *plan_out);
+/* VisionPatchProjectionBytesPlan::validate_capabilities (:1863-1885). */
+int32_t pvlc_hip_projection_validate_capabilities(const pvlc_hip_projection_plan *plan, int32_t shader_f16_available,
+                                                  uint32_t max_workgroups_per_dimension);
+/* VisionPatchProjectionBytesPlan::validate_operands (:1887-1905): exact byte
+ * lengths, then finite values (host memory, little-endian f32 / f16). */
+int32_t pvlc_hip_projection_validate_operands(const pvlc_hip_projection_plan *plan, const void *input,
+                                              size_t input_bytes, const void *weight, size_t weight_bytes,
+                                              const void *bias, size_t bias_bytes);
+
+/* Bytes of the workspace of pvlc_hip_linear_projection_f16 for rows x input_width. */
+size_t pvlc_hip_linear_projection_workspace_bytes(uint32_t rows, uint32_t input_width);
+/* out[r][n] = sum_k input[r][k] * weight[n][k] + bias[n]: f32 activations
+ * [rows][input_width], fp16 weights output-major [output_width][input_width],
+ * f32 bias and output [rows][output_width] -- linear_projection_f16_weights
+ * (pvlc-wgsl lib.rs:1836-1964, the prefill projection stages of runtime-core
+ * :2545-2560) with f32-grade products on MFMA (each activation row scaled by a
+ * power of two and split exactly into two fp16 halves).  Device pointers
+ * (16-byte aligned), caller stream, caller workspace (256-byte aligned),
+ * nothing allocated.  Admitted as the f16 plan above, plus input_width a
+ * multiple of 32 (the MFMA depth step); input-major weights are not taken. */
+pvlc_hip_status pvlc_hip_linear_projection_f16(const float *input, const uint16_t *weight, const float *bias,
+                                               float *output, uint32_t rows, uint32_t input_width,
+                                               uint32_t output_width, void *workspace, size_t workspace_bytes,
+                                               void *stream);
+
 #ifdef __cplusplus
 }
 #endif

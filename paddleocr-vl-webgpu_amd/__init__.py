@@ -97,6 +97,25 @@ class GqaSplitPlanC(ctypes.Structure):
                 ("merge_workgroups", _U32), ("uniform_words", _U32 * 4)]
 
 
+class ProjectionPlanC(ctypes.Structure):
+    _fields_ = [("kernel", _U32), ("weight_storage", _U32), ("input_bytes", ctypes.c_uint64),
+                ("weight_bytes", ctypes.c_uint64), ("bias_bytes", ctypes.c_uint64), ("output_bytes", ctypes.c_uint64),
+                ("dispatch", _U32 * 3)]
+
+
+# VisionPatchProjectionBytesErrorCode (runtime-core lib.rs:1751-1759).
+PROJECTION_ERROR_CODES = {1: "InvalidGeometry", 2: "Overflow", 3: "LengthMismatch", 4: "NonFinite",
+                          5: "MissingShaderF16", 6: "DispatchLimitExceeded"}
+
+
+class ProjectionPlanError(Exception):
+    """VisionPatchProjectionBytesError (runtime-core lib.rs:1761-1766)."""
+
+    def __init__(self, code: int):
+        self.code = PROJECTION_ERROR_CODES.get(code, str(code))
+        super().__init__(f"vision patch-projection bytes error {self.code}")
+
+
 class GemvTiledPlanC(ctypes.Structure):
     _fields_ = [("tile_rows", _U32), ("threads_per_row", _U32), ("vector_width", _U32), ("shared_capacity", _U32),
                 ("workgroup_storage_bytes", _U32), ("dispatch", _U32 * 3), ("workgroup_size", _U32 * 3),
@@ -192,6 +211,13 @@ SIGNATURES = {
     "pvlc_hip_gemv_f16": ([_VP, _VP, _VP, _U32, _U32, _VP], ctypes.c_int32),
     "pvlc_hip_top1_workspace_bytes": ([], _SZ),
     "pvlc_hip_paged_prefill_workspace_bytes": ([_U32], _SZ),
+    "pvlc_hip_projection_plan_create": ([_U32, _U32, _U32, _U32, ctypes.POINTER(ProjectionPlanC)], ctypes.c_int32),
+    "pvlc_hip_projection_validate_capabilities": ([ctypes.POINTER(ProjectionPlanC), ctypes.c_int32, _U32],
+                                                  ctypes.c_int32),
+    "pvlc_hip_projection_validate_operands": ([ctypes.POINTER(ProjectionPlanC), _VP, _SZ, _VP, _SZ, _VP, _SZ],
+                                              ctypes.c_int32),
+    "pvlc_hip_linear_projection_workspace_bytes": ([_U32, _U32], _SZ),
+    "pvlc_hip_linear_projection_f16": ([_VP, _VP, _VP, _VP, _U32, _U32, _U32, _VP, _SZ, _VP], ctypes.c_int32),
     "pvlc_hip_logits_top1_f32": ([_VP, _U32, _VP, _VP, _SZ, _VP], ctypes.c_int32),
     "pvlc_hip_lm_head_top1_f16": ([_VP, _VP, _VP, _U32, _U32, _VP, _VP, _SZ, _VP], ctypes.c_int32),
 }
@@ -395,6 +421,61 @@ def lm_head_top1_f16(weights, hidden, logits, rows: int, columns: int, result, w
     """LM-head GEMV (gemv_f16 semantics) and the top-1 of its logits in one launch; logits may be None."""
     _check(lib.pvlc_hip_lm_head_top1_f16(_ptr(weights), _ptr(hidden), _ptr(logits), rows, columns, _ptr(result),
                                          _ptr(workspace), workspace_bytes, _stream(stream)))
+
+
+class ProjectionPlan:
+    """VisionPatchProjectionBytesPlan (runtime-core lib.rs:1741-1749) and its checks (:1853-1913)."""
+
+    def __init__(self, raw: ProjectionPlanC):
+        self._raw = raw
+        self.kernel = "linear_projection_f16_weights" if raw.kernel == 1 else "vision_patch_projection_f32"
+        self.weight_storage = "f16" if raw.weight_storage == 1 else "f32"
+        self.input_bytes, self.weight_bytes = raw.input_bytes, raw.weight_bytes
+        self.bias_bytes, self.output_bytes = raw.bias_bytes, raw.output_bytes
+        self.dispatch = list(raw.dispatch)
+
+    def requires_shader_f16(self) -> bool:
+        return self.weight_storage == "f16"
+
+    def validate_capabilities(self, shader_f16_available: bool, max_compute_workgroups_per_dimension: int) -> None:
+        rc = lib.pvlc_hip_projection_validate_capabilities(ctypes.byref(self._raw), int(shader_f16_available),
+                                                           max_compute_workgroups_per_dimension)
+        if rc:
+            raise ProjectionPlanError(rc)
+
+    def validate_operands(self, input: bytes, weight: bytes, bias: bytes) -> None:
+        args = []
+        keep = []
+        for data in (input, weight, bias):
+            data = bytes(data)
+            buf = ctypes.create_string_buffer(data, len(data)) if data else None
+            keep.append(buf)
+            args += [ctypes.cast(buf, _VP) if buf is not None else None, len(data)]
+        rc = lib.pvlc_hip_projection_validate_operands(ctypes.byref(self._raw), *args)
+        if rc:
+            raise ProjectionPlanError(rc)
+
+
+def plan_projection(patch_count: int, input_width: int, output_width: int, weight_storage: str = "f16") -> ProjectionPlan:
+    """VisionPatchProjectionBytesDescriptor::plan (runtime-core lib.rs:1768-1840)."""
+    raw = ProjectionPlanC()
+    rc = lib.pvlc_hip_projection_plan_create(patch_count, input_width, output_width,
+                                             1 if weight_storage == "f16" else 0, ctypes.byref(raw))
+    if rc:
+        raise ProjectionPlanError(rc)
+    return ProjectionPlan(raw)
+
+
+def linear_projection_workspace_bytes(rows: int, input_width: int) -> int:
+    return int(lib.pvlc_hip_linear_projection_workspace_bytes(rows, input_width))
+
+
+def linear_projection_f16(input, weight, bias, out, rows: int, input_width: int, output_width: int, workspace,
+                          workspace_bytes: int, stream=None) -> None:
+    """out = input . weight^T + bias with fp16 weights and f32 activations (linear_projection_f16_weights,
+    pvlc-wgsl lib.rs:1836-1964), f32-grade products on MFMA."""
+    _check(lib.pvlc_hip_linear_projection_f16(_ptr(input), _ptr(weight), _ptr(bias), _ptr(out), rows, input_width,
+                                              output_width, _ptr(workspace), workspace_bytes, _stream(stream)))
 
 
 def plan_prefill(tokens: int, cache_capacity: int) -> None:

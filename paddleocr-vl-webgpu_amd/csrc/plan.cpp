@@ -348,6 +348,36 @@ int plan_gemv_tiled(uint32_t rows, uint32_t columns, pvlc_hip_gemv_tiled_plan *o
     return ok();
 }
 
+// VisionPatchProjectionBytesDescriptor::plan, runtime-core lib.rs:1768-1840.
+int32_t plan_projection(uint32_t patch_count, uint32_t input_width, uint32_t output_width, uint32_t weight_storage,
+                        pvlc_hip_projection_plan *out) {
+    if (patch_count == 0 || input_width == 0 || output_width == 0) return PVLC_HIP_PROJ_INVALID_GEOMETRY;
+    const bool f16 = weight_storage == 1;
+    if (f16 && (input_width % 4 != 0 || output_width % 4 != 0)) return PVLC_HIP_PROJ_INVALID_GEOMETRY;
+    // u32 x u32 fits in u64; the byte counts are the checked multiplications
+    const uint64_t input_elements = static_cast<uint64_t>(patch_count) * input_width;
+    const uint64_t weight_elements = static_cast<uint64_t>(output_width) * input_width;
+    const uint64_t output_elements = static_cast<uint64_t>(patch_count) * output_width;
+    uint64_t input_bytes = 0, weight_bytes = 0, output_bytes = 0;
+    if (__builtin_mul_overflow(input_elements, uint64_t{4}, &input_bytes) ||
+        __builtin_mul_overflow(weight_elements, uint64_t{f16 ? 2u : 4u}, &weight_bytes) ||
+        __builtin_mul_overflow(output_elements, uint64_t{4}, &output_bytes))
+        return PVLC_HIP_PROJ_OVERFLOW;
+    pvlc_hip_projection_plan p{};
+    p.kernel = f16 ? 1u : 0u;
+    p.weight_storage = f16 ? 1u : 0u;
+    p.input_bytes = input_bytes;
+    p.weight_bytes = weight_bytes;
+    p.bias_bytes = static_cast<uint64_t>(output_width) * 4;
+    p.output_bytes = output_bytes;
+    auto ceil_div = [](uint32_t v, uint32_t d) { return v / d + (v % d != 0); };  // lib.rs:5295-5297
+    p.dispatch[0] = ceil_div(output_width, 32);
+    p.dispatch[1] = ceil_div(patch_count, 32);
+    p.dispatch[2] = 1;
+    if (out) *out = p;
+    return PVLC_HIP_PROJ_OK;
+}
+
 DecodeShape decode_shape(uint32_t partition_tokens, bool streaming) {
     const uint32_t tiles = (partition_tokens + kBlockTokens - 1) / kBlockTokens;
     if (streaming) return tiles >= 8 ? DecodeShape{4, 1} : DecodeShape{2, 1};
@@ -413,6 +443,58 @@ extern "C" {
 pvlc_hip_status pvlc_hip_gemv_tiled_plan_create(uint32_t rows, uint32_t columns, pvlc_hip_gemv_tiled_plan *plan_out) {
     if (!plan_out) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "plan output is NULL");
     return plan_gemv_tiled(rows, columns, plan_out);
+}
+
+int32_t pvlc_hip_projection_plan_create(uint32_t patch_count, uint32_t input_width, uint32_t output_width,
+                                        uint32_t weight_storage, pvlc_hip_projection_plan *plan_out) {
+    if (weight_storage > 1) return PVLC_HIP_PROJ_INVALID_GEOMETRY;
+    return pvlc::plan_projection(patch_count, input_width, output_width, weight_storage, plan_out);
+}
+
+int32_t pvlc_hip_projection_validate_capabilities(const pvlc_hip_projection_plan *plan, int32_t shader_f16_available,
+                                                  uint32_t max_workgroups_per_dimension) {
+    // VisionPatchProjectionBytesPlan::validate_capabilities, lib.rs:1863-1885
+    if (!plan) return PVLC_HIP_PROJ_INVALID_GEOMETRY;
+    if (plan->weight_storage == 1 && !shader_f16_available) return PVLC_HIP_PROJ_MISSING_SHADER_F16;
+    if (max_workgroups_per_dimension == 0 || plan->dispatch[0] > max_workgroups_per_dimension ||
+        plan->dispatch[1] > max_workgroups_per_dimension)
+        return PVLC_HIP_PROJ_DISPATCH_LIMIT_EXCEEDED;
+    return PVLC_HIP_PROJ_OK;
+}
+
+int32_t pvlc_hip_projection_validate_operands(const pvlc_hip_projection_plan *plan, const void *input,
+                                              size_t input_bytes, const void *weight, size_t weight_bytes,
+                                              const void *bias, size_t bias_bytes) {
+    // VisionPatchProjectionBytesPlan::validate_operands, lib.rs:1887-1913:
+    // every length first (input, weight, bias), then finiteness in the same order
+    if (!plan) return PVLC_HIP_PROJ_INVALID_GEOMETRY;
+    if (input_bytes != plan->input_bytes || weight_bytes != plan->weight_bytes || bias_bytes != plan->bias_bytes)
+        return PVLC_HIP_PROJ_LENGTH_MISMATCH;
+    if ((input_bytes && !input) || (weight_bytes && !weight) || (bias_bytes && !bias))
+        return PVLC_HIP_PROJ_LENGTH_MISMATCH;
+    auto finite_f32 = [](const void *bytes, size_t n) {
+        const unsigned char *b = static_cast<const unsigned char *>(bytes);
+        for (size_t i = 0; i + 4 <= n; i += 4) {
+            uint32_t v;
+            std::memcpy(&v, b + i, 4);
+            if ((v & 0x7f800000u) == 0x7f800000u) return false;
+        }
+        return true;
+    };
+    auto finite_f16 = [](const void *bytes, size_t n) {
+        const unsigned char *b = static_cast<const unsigned char *>(bytes);
+        for (size_t i = 0; i + 2 <= n; i += 2) {
+            uint16_t v;
+            std::memcpy(&v, b + i, 2);
+            if ((v & 0x7c00u) == 0x7c00u) return false;
+        }
+        return true;
+    };
+    if (!finite_f32(input, input_bytes)) return PVLC_HIP_PROJ_NON_FINITE;
+    if (plan->weight_storage == 1 ? !finite_f16(weight, weight_bytes) : !finite_f32(weight, weight_bytes))
+        return PVLC_HIP_PROJ_NON_FINITE;
+    if (!finite_f32(bias, bias_bytes)) return PVLC_HIP_PROJ_NON_FINITE;
+    return PVLC_HIP_PROJ_OK;
 }
 
 const char *pvlc_hip_last_error_message(void) { return g_last_error.c_str(); }

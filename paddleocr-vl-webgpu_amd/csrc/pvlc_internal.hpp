@@ -98,6 +98,24 @@ int launch_kv_unpack(const uint16_t *key_cache, const uint16_t *value_cache, uin
                      uint32_t num_blocks, uint16_t *key_rows, uint16_t *value_rows, void *stream);
 int launch_prefill(const pvlc_hip_paged_prefill_args *args, void *stream);
 
+// Prefill projection with fp16 weights: workspace of the exact hi/lo split
+// of the activations ([rows][K] fp16 each) and the per-row exponents.
+struct ProjectionWorkspace {
+    uint16_t *hi;
+    uint16_t *lo;
+    int32_t *exponents;
+};
+struct ProjectionWorkspaceLayout {
+    size_t lo_offset, exponents_offset, total;
+};
+inline ProjectionWorkspaceLayout projection_workspace_layout(uint32_t rows, uint32_t k_width) {
+    const size_t plane = (static_cast<size_t>(rows) * k_width * 2 + 255) / 256 * 256;
+    return {plane, 2 * plane, 2 * plane + (static_cast<size_t>(rows) * 4 + 255) / 256 * 256};
+}
+int launch_linear_projection_f16(const float *input, const uint16_t *weight, const float *bias, float *out,
+                                 uint32_t rows, uint32_t k_width, uint32_t n_width, const ProjectionWorkspace &ws,
+                                 void *stream);
+
 // Split-K pair schedule of the causal prefill.  Query block qb (16 tokens)
 // of one kv head attends qb/4 + 1 steps of 64 keys, so a grid of one
 // workgroup per block is as long as its last block while most compute units
@@ -168,6 +186,11 @@ constexpr size_t kTop1WorkspaceBytes = kTop1Slots * sizeof(Top1Slot);
 int launch_gemv_top1_f16(const uint16_t *weights, const float *vector, float *logits, uint32_t rows,
                          uint32_t columns, Top1Slot *slots, uint32_t *result, void *stream);
 int launch_logits_top1_f32(const float *logits, uint32_t vocab, Top1Slot *slots, uint32_t *result, void *stream);
+
+// VisionPatchProjectionBytesDescriptor::plan (runtime-core lib.rs:1768-1840);
+// returns a pvlc_hip_projection_error.
+int32_t plan_projection(uint32_t patch_count, uint32_t input_width, uint32_t output_width, uint32_t weight_storage,
+                        pvlc_hip_projection_plan *out);
 
 // GemvTiledDescriptor::plan (runtime-core lib.rs:753-785); returns a status.
 int plan_gemv_tiled(uint32_t rows, uint32_t columns, pvlc_hip_gemv_tiled_plan *out);

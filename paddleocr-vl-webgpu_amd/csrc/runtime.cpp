@@ -527,6 +527,45 @@ pvlc_hip_status pvlc_hip_lm_head_top1_f16(const uint16_t *weights, const float *
     return ok();
 }
 
+size_t pvlc_hip_linear_projection_workspace_bytes(uint32_t rows, uint32_t input_width) {
+    if (rows == 0 || input_width == 0) return 0;
+    return projection_workspace_layout(rows, input_width).total;
+}
+
+pvlc_hip_status pvlc_hip_linear_projection_f16(const float *input, const uint16_t *weight, const float *bias,
+                                               float *output, uint32_t rows, uint32_t input_width,
+                                               uint32_t output_width, void *workspace, size_t workspace_bytes,
+                                               void *stream) {
+    if (!input || !weight || !bias || !output || !workspace)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "projection buffer pointer is NULL");
+    const int32_t pe = plan_projection(rows, input_width, output_width, 1, nullptr);
+    if (pe == PVLC_HIP_PROJ_OVERFLOW)
+        return invalid(PVLC_HIP_INV_ARITHMETIC_OVERFLOW, "projection byte geometry overflowed");
+    if (pe != PVLC_HIP_PROJ_OK)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY,
+                       "projection geometry must be positive with widths a multiple of 4");
+    if (input_width % 32 != 0)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "device projection needs input_width a multiple of 32");
+    if (rows > 65535u * 128u)
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "projection rows exceed the grid");
+    for (const void *ptr : {static_cast<const void *>(input), static_cast<const void *>(weight),
+                            static_cast<const void *>(output)})
+        if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0)
+            return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "projection input, weight and output must be 16-byte aligned");
+    const ProjectionWorkspaceLayout layout = projection_workspace_layout(rows, input_width);
+    if (workspace_bytes < layout.total)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "projection workspace holds " + std::to_string(workspace_bytes) +
+                                                         " bytes but needs " + std::to_string(layout.total));
+    if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "projection workspace must be 256-byte aligned");
+    auto *base = static_cast<unsigned char *>(workspace);
+    const ProjectionWorkspace ws{reinterpret_cast<uint16_t *>(base), reinterpret_cast<uint16_t *>(base + layout.lo_offset),
+                                 reinterpret_cast<int32_t *>(base + layout.exponents_offset)};
+    const int e = launch_linear_projection_f16(input, weight, bias, output, rows, input_width, output_width, ws, stream);
+    if (e != 0) return hip_fail(static_cast<hipError_t>(e), "projection launch");
+    return ok();
+}
+
 size_t pvlc_hip_paged_decode_workspace_bytes(uint32_t num_seqs, uint32_t max_context, uint32_t partition_tokens) {
     if (num_seqs == 0 || max_context == 0) return 0;
     if (partition_tokens == 0) return decode_workspace_layout(num_seqs, auto_workspace_parts(num_seqs, max_context)).total;

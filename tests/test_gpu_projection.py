@@ -1,0 +1,88 @@
+"""GPU parity of the prefill projection with fp16 weights (linear_projection_f16_weights, pvlc-wgsl
+lib.rs:1836-1964) against the oracle's linear_f32 with a bias (cpu-ref lib.rs:88-140).
+
+The device computes each product as W.(hi + lo), where hi + lo is the activation row scaled by a power of
+two and split exactly into two fp16 values (~22 bits), on MFMA with f32 accumulation; the reference widens
+the fp16 weights and accumulates in f32.  Both are held to the standard error bound of an f32 dot product
+against an f64 evaluation, |y - y64| <= gamma_m * (sum|w*x| + |b|), gamma_m = m*u/(1-m*u), u = 2^-24 --
+m = K + 1 for the oracle's sequential sum, m = 2K + 2 for the device (two MFMA products per term) -- plus
+2^-21 * sum|w|*|x| for the split.  A dropped depth chunk, a wrong row or column, or a missing scale or
+bias is orders of magnitude outside that."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from pvlc_testlib import f16_bits, log, pvlc, to_dev, to_dev_f32, widen
+
+pytestmark = pytest.mark.gpu
+
+
+def bound_ratio(got, w, x, b, chain, split_term):
+    u = 2.0 ** -24
+    g = chain * u / (1 - chain * u)
+    w64, x64, b64 = np.asarray(w, np.float64), np.asarray(x, np.float64), np.asarray(b, np.float64)
+    exact = x64 @ w64.T + b64
+    mag = np.abs(x64) @ np.abs(w64).T + np.abs(b64)
+    allowed = g * mag + (2.0 ** -21 * (np.abs(x64) @ np.abs(w64).T) if split_term else 0.0)
+    err = np.abs(np.asarray(got, np.float64) - exact)
+    return float((err / np.maximum(allowed, 1e-300)).max())
+
+
+def run_projection(rows, k, n, seed, x=None, zero_bias=False):
+    import torch
+    w = f16_bits(seed, n * k, 0.05)
+    if x is None:
+        x = O.normal_f32(seed + 1, rows * k).reshape(rows, k)
+    b = np.zeros(n, np.float32) if zero_bias else O.normal_f32(seed + 2, n)
+    wsb = pvlc.linear_projection_workspace_bytes(rows, k)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    sentinel = -7.0
+    d_out = torch.full((rows * n + 64,), sentinel, dtype=torch.float32, device="cuda")
+    pvlc.linear_projection_f16(to_dev_f32(x), to_dev(w), to_dev_f32(b), d_out, rows, k, n, ws, wsb)
+    torch.cuda.synchronize()
+    got = d_out.cpu().numpy()
+    assert np.all(got[rows * n:] == sentinel), "projection wrote past the output"
+    return got[:rows * n].reshape(rows, n), widen(w).reshape(n, k), x, b
+
+
+def check(rows, k, n, got, wf, x, b, label, oracle_rows=None):
+    sel = np.arange(rows) if oracle_rows is None else np.asarray(oracle_rows)
+    ratio = bound_ratio(got[sel], wf, x[sel], b, 2 * k + 2, True)
+    log(f"[parity] projection {label}: max |gpu - f64| / bound = {ratio:.3f}")
+    assert np.all(np.isfinite(got))
+    assert ratio <= 1.0
+    if oracle_rows is None:
+        want = O.linear_f32(x, rows, k, wf, b, n).reshape(rows, n)
+        assert bound_ratio(want, wf, x, b, k + 1, False) <= 1.0  # the oracle inside its own bound
+
+
+# decoder prefill shapes (hidden 1024, q 2048, kv 256, MLP 3072) and ragged tiles
+@pytest.mark.parametrize("rows,k,n", [(1, 1024, 4), (37, 1024, 2048), (128, 1024, 256), (129, 1024, 260),
+                                      (300, 2048, 1024), (200, 3072, 1024), (77, 1024, 2560), (33, 1024, 6144)])
+def test_projection_matches_linear_oracle(rows, k, n):
+    log(f"case: projection rows={rows} k={k} n={n}")
+    got, wf, x, b = run_projection(rows, k, n, seed=rows * 31 + k + n)
+    check(rows, k, n, got, wf, x, b, f"{rows}x{k}x{n}")
+
+
+def test_projection_at_prefill_size_sampled_rows():
+    rows, k, n = 4096, 1024, 2560  # q|k|v of a 4096-token prefill as one matrix
+    log("case: projection 4096x1024x2560 (sampled rows)")
+    got, wf, x, b = run_projection(rows, k, n, seed=4096)
+    check(rows, k, n, got, wf, x, b, "4096x1024x2560", oracle_rows=[0, 1, 127, 128, 2047, 3000, 4094, 4095])
+
+
+def test_rows_far_outside_the_fp16_range_keep_f32_accuracy():
+    rows, k, n = 6, 1024, 64
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x[0] *= np.float32(1e30)   # beyond fp16 (the power-of-two scaling brings it in range)
+    x[1] *= np.float32(1e-20)  # far below fp16 normals
+    x[2] = 0.0                 # an all-zero row
+    x[3, 5] = np.float32(3e20)  # one huge element among ordinary ones
+    x[4] = np.float32(65504.0 * 4)
+    log("case: projection dynamic range")
+    got, wf, xx, b = run_projection(rows, k, n, seed=77, x=x, zero_bias=True)
+    check(rows, k, n, got, wf, xx, b, "dynamic range")
+    np.testing.assert_array_equal(got[2], b)
