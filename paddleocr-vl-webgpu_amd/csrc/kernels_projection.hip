@@ -12,13 +12,15 @@
 // then give f32-grade sums at half the fp16 MFMA rate; the epilogue multiplies
 // by 2^e (exact) and adds the bias.
 //
-// Kernel 1 (split): one workgroup per row: the row maximum, the exponent, the
-// hi/lo planes [rows][K] in the workspace.
+// Kernel 1 (split): one workgroup per 8 rows: the row maxima, the exponents,
+// and the hi/lo planes written in the GEMM's tile order (per 128-row tile and
+// 32-wide k step one 16 KiB block [plane][k-chunk (4)][row (128)][8]), so a
+// GEMM stage of the activations is one contiguous 16 KiB run.
 // Kernel 2 (GEMM): 128 x 128 output tiles, K in steps of 32, 4 waves of
 // 64 x 64 (4 x 4 MFMA tiles of v_mfma_f32_16x16x32_f16 each, hi and lo);
-// hi, lo and weight tiles move by direct global-to-LDS loads into
-// [k-chunk][row][8] layouts (every operand read of 16 lanes is one 256-byte
-// run), through a three-stage ring with one barrier per step.
+// operand tiles move by direct global-to-LDS loads through a three-stage
+// ring with one barrier per step.  Every load instruction reads long runs:
+// 1 KiB of the activation block, or 16 weight rows x 64 bytes.
 
 #include <hip/hip_runtime.h>
 
@@ -31,10 +33,12 @@ namespace pvlc {
 namespace {
 
 constexpr int kSplitThreads = 256;
-constexpr int kTileM = 128, kTileN = 128, kTileK = 32;
+constexpr int kSplitRows = 8;  // rows per split workgroup: 8 x 16 bytes = one 128-byte line per chunk
+constexpr int kTileM = kProjectionTileRows, kTileN = 128, kTileK = kProjectionStepK;
 constexpr int kGemmThreads = 256;
 constexpr uint32_t kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 constexpr int kTileElems = kTileM * kTileK;  // fp16 elements of one 128 x 32 operand tile
+constexpr int kBlockElems = 2 * kTileElems;  // one activation block: hi and lo planes
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0, expcnt 6:4, lgkmcnt
 // 11:8, the last two left at their maximum) -- as builtins, so the compiler's
 // own wait insertion knows which loads they retire.
@@ -49,48 +53,99 @@ __device__ inline int split_exponent(float m) {
     return x - 14;
 }
 
+// Offset (fp16 elements) of row r, k-chunk c (8 elements) in the tile-ordered
+// planes: block (r / 128, c / 4), plane hi; lo is kTileElems further.
+__device__ inline size_t plane_offset(uint32_t r, uint32_t c, uint32_t steps) {
+    const size_t block = static_cast<size_t>(r / kTileM) * steps + c / 4;
+    return block * kBlockElems + ((c % 4) * kTileM + r % kTileM) * 8;
+}
+
+// Thread t of the workgroup serves row 8 g + t % 8 and the k-chunks t / 8 +
+// 32 i; the 8 threads of one chunk write one whole 128-byte line of each
+// plane.  Rows past the end (padding of the last tile) are written as zeros.
+// CPT > 0: K = 256 CPT, the thread's CPT chunks stay in registers between the
+// row maximum and the split (one pass over the input); CPT = 0: any K that is
+// a multiple of 32, the chunks are read again for the split.
+template <int CPT>
 __global__ __launch_bounds__(kSplitThreads) void projection_split_kernel(const float *__restrict__ input,
-                                                                        uint32_t k_width, uint16_t *__restrict__ hi,
-                                                                        uint16_t *__restrict__ lo,
+                                                                        uint32_t rows, uint32_t k_width,
+                                                                        uint16_t *__restrict__ tiles,
                                                                         int32_t *__restrict__ exponents) {
-    const size_t row = blockIdx.x;
-    const float *in = input + row * k_width;
+    const uint32_t rr = threadIdx.x % kSplitRows, c0 = threadIdx.x / kSplitRows;
+    constexpr uint32_t kChunkStride = kSplitThreads / kSplitRows;
+    const uint32_t row = blockIdx.x * kSplitRows + rr, chunks = k_width / 8, steps = k_width / kTileK;
+    const bool live = row < rows;
+    const float *in = input + static_cast<size_t>(live ? row : 0) * k_width;
+    auto load = [&](uint32_t c, float4_t &a, float4_t &b) {
+        a = *reinterpret_cast<const float4_t *>(in + c * 8);
+        b = *reinterpret_cast<const float4_t *>(in + c * 8 + 4);
+    };
+    auto chunk_max = [](float m, const float4_t &a, const float4_t &b) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(a[j]), fabsf(b[j])));
+        return m;
+    };
     float m = 0.f;
-    for (uint32_t k = threadIdx.x * 4; k < k_width; k += kSplitThreads * 4) {
-        const float4_t v = *reinterpret_cast<const float4_t *>(in + k);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-    }
+    float4_t va[CPT > 0 ? CPT : 1], vb[CPT > 0 ? CPT : 1];
+    if constexpr (CPT > 0) {
+        // Padding rows read row 0 (every load unconditional) and are zeroed below.
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    __shared__ float sm_max[kSplitThreads / 64];
-    if ((threadIdx.x & 63) == 0) sm_max[threadIdx.x >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(sm_max[0], sm_max[1]), fmaxf(sm_max[2], sm_max[3]));
-    const int e = split_exponent(m);
-    if (threadIdx.x == 0) exponents[row] = e;
-    for (uint32_t k = threadIdx.x * 4; k < k_width; k += kSplitThreads * 4) {
-        const float4_t v = *reinterpret_cast<const float4_t *>(in + k);
-        u16x4_t h, l;
+        for (int i = 0; i < CPT; ++i) load(c0 + i * kChunkStride, va[i], vb[i]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float s = __builtin_ldexpf(v[j], -e);  // exact: a power of two
-            const _Float16 sh = to_h(s);
-            h[j] = __builtin_bit_cast(uint16_t, sh);
-            l[j] = __builtin_bit_cast(uint16_t, to_h(s - static_cast<float>(sh)));  // the remainder is exact in f32
+        for (int i = 0; i < CPT; ++i) m = chunk_max(m, va[i], vb[i]);
+        if (!live) m = 0.f;
+    } else if (live) {
+        for (uint32_t c = c0; c < chunks; c += kChunkStride) {
+            float4_t a, b;
+            load(c, a, b);
+            m = chunk_max(m, a, b);
         }
-        *reinterpret_cast<u16x4_t *>(hi + row * k_width + k) = h;
-        *reinterpret_cast<u16x4_t *>(lo + row * k_width + k) = l;
+    }
+    // Lanes of one row differ in lane bits 3..5; then the 4 waves.
+#pragma unroll
+    for (int o = 8; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    __shared__ float sm_max[kSplitThreads / 64][kSplitRows];
+    if ((threadIdx.x & 63) < kSplitRows) sm_max[threadIdx.x >> 6][rr] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(sm_max[0][rr], sm_max[1][rr]), fmaxf(sm_max[2][rr], sm_max[3][rr]));
+    const int e = split_exponent(m);
+    if (threadIdx.x < kSplitRows) exponents[row] = e;
+    auto split_store = [&](uint32_t c, const float4_t &a, const float4_t &b) {
+        half8_t h, l;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float s = live ? __builtin_ldexpf(j < 4 ? a[j] : b[j - 4], -e) : 0.f;  // exact: a power of two
+            h[j] = to_h(s);
+            l[j] = to_h(s - static_cast<float>(h[j]));  // the remainder is exact in f32
+        }
+        const size_t off = plane_offset(row, c, steps);
+        *reinterpret_cast<half8_t *>(tiles + off) = h;
+        *reinterpret_cast<half8_t *>(tiles + off + kTileElems) = l;
+    };
+    if constexpr (CPT > 0) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) split_store(c0 + i * kChunkStride, va[i], vb[i]);
+    } else {
+        for (uint32_t c = c0; c < chunks; c += kChunkStride) {
+            float4_t a = {0.f, 0.f, 0.f, 0.f}, b = a;
+            if (live) load(c, a, b);
+            split_store(c, a, b);
+        }
     }
 }
 
-// LDS tile layout [k-chunk (4)][row (128)][8]: the fragment a 16-lane group
-// reads (16 rows, one 8-element chunk) is one contiguous 256-byte run.
-__device__ inline int tile_offset(int kchunk, int row) { return (kchunk * kTileM + row) * 8; }
+// LDS layouts.  Activations: the block as stored, [plane][k-chunk (4)][row
+// (128)][8], so the fragment a 16-lane group reads (16 rows, one chunk) is one
+// 256-byte run.  Weights: [row (128)][slot (4)][8] with k-chunk c of row r in
+// slot c ^ ((r / 4) % 4): the 4 slots of a row are one 64-byte run of the
+// weight row (one load of 4 lanes), and the 16 rows of a fragment read (one
+// chunk each) fall on 16 distinct 16-byte bank groups.
+__device__ inline int a_offset(int kchunk, int row) { return (kchunk * kTileM + row) * 8; }
+__device__ inline int w_offset(int kchunk, int row) { return (row * 4 + (kchunk ^ ((row >> 2) & 3))) * 8; }
 
 __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_kernel(
-    const uint16_t *__restrict__ hi, const uint16_t *__restrict__ lo, const int32_t *__restrict__ exponents,
-    const uint16_t *__restrict__ weight, const float *__restrict__ bias, float *__restrict__ out, uint32_t rows,
-    uint32_t k_width, uint32_t n_width) {
+    const uint16_t *__restrict__ tiles, const int32_t *__restrict__ exponents, const uint16_t *__restrict__ weight,
+    const float *__restrict__ bias, float *__restrict__ out, uint32_t rows, uint32_t k_width, uint32_t n_width) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int row16 = lane & 15, kg = lane >> 4;
@@ -102,38 +157,47 @@ __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_kernel(
     const uint32_t total = gridDim.x, xcd = blockIdx.x % kXcds, idx = blockIdx.x / kXcds;
     const uint32_t q = total / kXcds, r = total % kXcds;
     const uint32_t tile = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
-    const uint32_t m0 = (tile / n_tiles) * kTileM, n0 = (tile % n_tiles) * kTileN;
+    const uint32_t mt = tile / n_tiles, m0 = mt * kTileM, n0 = (tile % n_tiles) * kTileN;
     const int wm = wave >> 1, wn = wave & 1;  // the wave's 64 x 64 quadrant
+    const uint32_t steps = k_width / kTileK;
 
     // Three-stage ring of distinct LDS arrays (picked at compile time in the
     // loop unrolled by three): step s computes stage s while the loads of
     // stage s+1 and s+2 are in flight, and its closing barrier waits only for
     // stage s+1 (vmcnt(6): the 6 loads per thread of stage s+2 may still be
     // outstanding).  Loads of stage 1 and of stage s+2 beyond the last clamp
-    // to the last stage, so a single-step K is also exact.  The compiler sees that loads into one array and reads of
-    // another do not alias, so it adds no wait of its own before the reads.
-    __shared__ uint16_t sh0[kTileElems], sl0[kTileElems], sw0[kTileElems];
-    __shared__ uint16_t sh1[kTileElems], sl1[kTileElems], sw1[kTileElems];
-    __shared__ uint16_t sh2[kTileElems], sl2[kTileElems], sw2[kTileElems];
+    // to the last stage, so a single-step K is also exact.  The compiler sees
+    // that loads into one array and reads of another do not alias, so it adds
+    // no wait of its own before the reads.
+    __shared__ uint16_t sa0[kBlockElems], sw0[kTileElems];
+    __shared__ uint16_t sa1[kBlockElems], sw1[kTileElems];
+    __shared__ uint16_t sa2[kBlockElems], sw2[kTileElems];
     typedef __attribute__((address_space(3))) void *lds_ptr;
 
-    // Direct global-to-LDS loads: LDS chunk q = 64 j + lane of a tile holds
-    // k-chunk q / 128 of tile row q % 128.  Each wave moves 2 of the 8
-    // instructions per tile (6 loads per thread per stage).  Rows past the
-    // end re-read the last row (never stored).
-    const uint32_t last_row = rows - 1, last_col = n_width - 1;
-    auto stage = [&](uint32_t k0, uint16_t *dh, uint16_t *dl, uint16_t *dw) {
+    // Direct global-to-LDS loads, 64 lanes x 16 bytes per instruction, lane l
+    // landing at 16 l of the instruction's 1 KiB.  Activations: the 16 KiB
+    // block (tile mt, step s) as 16 instructions of 1 KiB, 4 per wave.
+    // Weights: 8 instructions of 16 rows each, 2 per wave; lane l of
+    // instruction j fills LDS slot p = 64 j + l, i.e. row p / 4, slot p % 4.
+    // Weight rows past the end re-read the last row (never stored).
+    const uint16_t *a_tiles = tiles + static_cast<size_t>(mt) * steps * kBlockElems + (wave * 4) * 512 + lane * 8;
+    const uint32_t last_col = n_width - 1;
+    size_t w_row_off[2];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int j = wave * 2 + r;
-            const int q = 64 * j + lane;
-            const uint32_t trow = static_cast<uint32_t>(q & 127), kc = static_cast<uint32_t>(q >> 7);
-            const size_t a_off = static_cast<size_t>(min(m0 + trow, last_row)) * k_width + k0 + kc * 8;
-            const size_t w_off = static_cast<size_t>(min(n0 + trow, last_col)) * k_width + k0 + kc * 8;
-            __builtin_amdgcn_global_load_lds(hi + a_off, (lds_ptr)(dh + 64 * j * 8), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(lo + a_off, (lds_ptr)(dl + 64 * j * 8), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(weight + w_off, (lds_ptr)(dw + 64 * j * 8), 16, 0, 0);
-        }
+    for (int rw = 0; rw < 2; ++rw) {
+        const int p = 64 * (wave * 2 + rw) + lane, wrow = p >> 2;
+        const int kc = (p & 3) ^ ((wrow >> 2) & 3);
+        w_row_off[rw] = static_cast<size_t>(min(n0 + wrow, last_col)) * k_width + kc * 8;
+    }
+    auto stage = [&](uint32_t s, uint16_t *da, uint16_t *dw) {
+        const uint16_t *a = a_tiles + static_cast<size_t>(s) * kBlockElems;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            __builtin_amdgcn_global_load_lds(a + j * 512, (lds_ptr)(da + (wave * 4 + j) * 512), 16, 0, 0);
+#pragma unroll
+        for (int rw = 0; rw < 2; ++rw)
+            __builtin_amdgcn_global_load_lds(weight + w_row_off[rw] + s * kTileK,
+                                             (lds_ptr)(dw + (wave * 2 + rw) * 512), 16, 0, 0);
     };
 
     float4_t acc[4][4];
@@ -144,46 +208,56 @@ __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_kernel(
 
     // 16 x 16 x 32 tiles: A = activations (lane row = l % 16, k = (l / 16) * 8 ..),
     // B = W^T (lane column = l % 16, same k), C: column l % 16, rows (l / 16) * 4 + i.
-    auto compute = [&](const uint16_t *sh, const uint16_t *sl, const uint16_t *sw) {
+    auto compute = [&](const uint16_t *sa, const uint16_t *sw) {
         half8_t bf[4];
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
-            bf[cb] = *reinterpret_cast<const half8_t *>(sw + tile_offset(kg, wn * 64 + cb * 16 + row16));
+            bf[cb] = *reinterpret_cast<const half8_t *>(sw + w_offset(kg, wn * 64 + cb * 16 + row16));
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             const int trow = wm * 64 + rb * 16 + row16;
-            const half8_t ah = *reinterpret_cast<const half8_t *>(sh + tile_offset(kg, trow));
-            const half8_t al = *reinterpret_cast<const half8_t *>(sl + tile_offset(kg, trow));
+            const half8_t ah = *reinterpret_cast<const half8_t *>(sa + a_offset(kg, trow));
+            const half8_t al = *reinterpret_cast<const half8_t *>(sa + kTileElems + a_offset(kg, trow));
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
+            for (int cb = 0; cb < 4; ++cb)
                 acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bf[cb], acc[rb][cb], 0, 0, 0);
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
                 acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[cb], acc[rb][cb], 0, 0, 0);
-            }
         }
+        // Schedule: the 12 fragment reads first, then the 32 MFMAs with the
+        // step's 6 global-to-LDS loads spread among them (masks: 0x100 LDS
+        // read, 0x008 MFMA, 0x020 global load).
+        __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     };
     // Step s: load stage s+2 (past the end: the last stage again, into the
     // buffer step s-1 freed, never read), compute stage s, wait for stage s+1,
     // barrier.  Unconditional loads keep the waits exact.
-    const uint32_t steps = k_width / kTileK;
-    auto step = [&](uint32_t s, uint16_t *ch, uint16_t *cl, uint16_t *cw, uint16_t *nh, uint16_t *nl, uint16_t *nw) {
-        stage(min(s + 2, steps - 1) * kTileK, nh, nl, nw);
-        compute(ch, cl, cw);
+    auto step = [&](uint32_t s, uint16_t *ca, uint16_t *cw, uint16_t *na, uint16_t *nw) {
+        stage(min(s + 2, steps - 1), na, nw);
+        compute(ca, cw);
         __builtin_amdgcn_s_waitcnt(kWaitVm6);
         __builtin_amdgcn_s_barrier();
     };
 
-    stage(0, sh0, sl0, sw0);
-    stage(min(1u, steps - 1) * kTileK, sh1, sl1, sw1);
+    stage(0, sa0, sw0);
+    stage(min(1u, steps - 1), sa1, sw1);
     __builtin_amdgcn_s_waitcnt(kWaitVm6);
     __builtin_amdgcn_s_barrier();
     uint32_t s = 0;
     for (; s + 3 <= steps; s += 3) {
-        step(s, sh0, sl0, sw0, sh2, sl2, sw2);
-        step(s + 1, sh1, sl1, sw1, sh0, sl0, sw0);
-        step(s + 2, sh2, sl2, sw2, sh1, sl1, sw1);
+        step(s, sa0, sw0, sa2, sw2);
+        step(s + 1, sa1, sw1, sa0, sw0);
+        step(s + 2, sa2, sw2, sa1, sw1);
     }
-    if (s < steps) step(s, sh0, sl0, sw0, sh2, sl2, sw2);
-    if (s + 1 < steps) step(s + 1, sh1, sl1, sw1, sh0, sl0, sw0);
+    if (s < steps) step(s, sa0, sw0, sa2, sw2);
+    if (s + 1 < steps) step(s + 1, sa1, sw1, sa0, sw0);
     __builtin_amdgcn_s_waitcnt(kWaitVm0);  // no load into LDS outlives the loop
 
     // Epilogue: x 2^e of the row (exact), + bias, f32 stores.
@@ -209,11 +283,18 @@ int launch_linear_projection_f16(const float *input, const uint16_t *weight, con
                                  uint32_t rows, uint32_t k_width, uint32_t n_width, const ProjectionWorkspace &ws,
                                  void *stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(projection_split_kernel, dim3(rows), dim3(kSplitThreads), 0, st, input, k_width, ws.hi, ws.lo,
-                       ws.exponents);
+    const uint32_t m_tiles = (rows + kTileM - 1) / kTileM;
+    const dim3 split_grid(m_tiles * (kTileM / kSplitRows));
+    switch (k_width) {
+    case 1024: hipLaunchKernelGGL(projection_split_kernel<4>, split_grid, dim3(kSplitThreads), 0, st, input, rows, k_width, ws.tiles, ws.exponents); break;
+    case 2048: hipLaunchKernelGGL(projection_split_kernel<8>, split_grid, dim3(kSplitThreads), 0, st, input, rows, k_width, ws.tiles, ws.exponents); break;
+    case 3072: hipLaunchKernelGGL(projection_split_kernel<12>, split_grid, dim3(kSplitThreads), 0, st, input, rows, k_width, ws.tiles, ws.exponents); break;
+    case 4096: hipLaunchKernelGGL(projection_split_kernel<16>, split_grid, dim3(kSplitThreads), 0, st, input, rows, k_width, ws.tiles, ws.exponents); break;
+    default: hipLaunchKernelGGL(projection_split_kernel<0>, split_grid, dim3(kSplitThreads), 0, st, input, rows, k_width, ws.tiles, ws.exponents); break;
+    }
     if (hipError_t e = hipGetLastError()) return static_cast<int>(e);
-    const uint32_t tiles = ((n_width + kTileN - 1) / kTileN) * ((rows + kTileM - 1) / kTileM);
-    hipLaunchKernelGGL(projection_gemm_kernel, dim3(tiles), dim3(kGemmThreads), 0, st, ws.hi, ws.lo, ws.exponents, weight,
+    const uint32_t tiles = ((n_width + kTileN - 1) / kTileN) * m_tiles;
+    hipLaunchKernelGGL(projection_gemm_kernel, dim3(tiles), dim3(kGemmThreads), 0, st, ws.tiles, ws.exponents, weight,
                        bias, out, rows, k_width, n_width);
     return static_cast<int>(hipGetLastError());
 }

@@ -100,17 +100,22 @@ int launch_prefill(const pvlc_hip_paged_prefill_args *args, void *stream);
 
 // Prefill projection with fp16 weights: workspace of the exact hi/lo split
 // of the activations ([rows][K] fp16 each) and the per-row exponents.
+// Workspace of the projection: the hi/lo planes of the split activations in
+// the GEMM's tile order -- for each 128-row tile t and each 32-wide k step s
+// one 16 KiB block [plane (hi, lo)][k-chunk (4)][row (128)][8 fp16] -- then
+// one exponent per row; rows are padded to a multiple of 128 (zeros).
+constexpr uint32_t kProjectionTileRows = 128, kProjectionStepK = 32;
 struct ProjectionWorkspace {
-    uint16_t *hi;
-    uint16_t *lo;
+    uint16_t *tiles;
     int32_t *exponents;
 };
 struct ProjectionWorkspaceLayout {
-    size_t lo_offset, exponents_offset, total;
+    size_t exponents_offset, total;
 };
 inline ProjectionWorkspaceLayout projection_workspace_layout(uint32_t rows, uint32_t k_width) {
-    const size_t plane = (static_cast<size_t>(rows) * k_width * 2 + 255) / 256 * 256;
-    return {plane, 2 * plane, 2 * plane + (static_cast<size_t>(rows) * 4 + 255) / 256 * 256};
+    const size_t padded = (static_cast<size_t>(rows) + kProjectionTileRows - 1) / kProjectionTileRows * kProjectionTileRows;
+    const size_t tiles = padded * k_width * 4;  // two fp16 planes
+    return {tiles, tiles + (padded * 4 + 255) / 256 * 256};
 }
 int launch_linear_projection_f16(const float *input, const uint16_t *weight, const float *bias, float *out,
                                  uint32_t rows, uint32_t k_width, uint32_t n_width, const ProjectionWorkspace &ws,

@@ -559,7 +559,7 @@ pvlc_hip_status pvlc_hip_linear_projection_f16(const float *input, const uint16_
     if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
         return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "projection workspace must be 256-byte aligned");
     auto *base = static_cast<unsigned char *>(workspace);
-    const ProjectionWorkspace ws{reinterpret_cast<uint16_t *>(base), reinterpret_cast<uint16_t *>(base + layout.lo_offset),
+    const ProjectionWorkspace ws{reinterpret_cast<uint16_t *>(base),
                                  reinterpret_cast<int32_t *>(base + layout.exponents_offset)};
     const int e = launch_linear_projection_f16(input, weight, bias, output, rows, input_width, output_width, ws, stream);
     if (e != 0) return hip_fail(static_cast<hipError_t>(e), "projection launch");

@@ -59,7 +59,9 @@ def check(rows, k, n, got, wf, x, b, label, oracle_rows=None):
 
 # decoder prefill shapes (hidden 1024, q 2048, kv 256, MLP 3072) and ragged tiles
 @pytest.mark.parametrize("rows,k,n", [(1, 1024, 4), (37, 1024, 2048), (128, 1024, 256), (129, 1024, 260),
-                                      (300, 2048, 1024), (200, 3072, 1024), (77, 1024, 2560), (33, 1024, 6144)])
+                                      (300, 2048, 1024), (200, 3072, 1024), (77, 1024, 2560), (33, 1024, 6144),
+                                      # widths off the K-specialised split (one k step, odd steps) and K = 4096
+                                      (130, 32, 132), (9, 96, 36), (140, 1056, 200), (70, 4096, 136)])
 def test_projection_matches_linear_oracle(rows, k, n):
     log(f"case: projection rows={rows} k={k} n={n}")
     got, wf, x, b = run_projection(rows, k, n, seed=rows * 31 + k + n)
