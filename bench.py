@@ -585,6 +585,9 @@ def bench_projection(args):
         total_flops += flops
         total_ms += ms
     tflops = total_flops / (total_ms * 1e-3) / 1e12
+    extra = {}
+    if not args.no_cpu:
+        extra["cpu_baseline"] = projection_cpu_baseline(calls, n, args.cpu_seconds, total_flops)
     print(json.dumps({
         "metric": "prefill projections of one decoder layer µs + TFLOP/s (N=4096, fp16 weights, f32 activations)",
         "value": round(total_ms * 1e3, 2), "unit": "µs/layer", "steps": min(args.steps, 50), "warmup": args.warmup,
@@ -594,8 +597,35 @@ def bench_projection(args):
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tflops / 2500.0, 4),
                      "note": "algorithmic FLOPs (2*N*out*in); the device issues two fp16 MFMAs per product, so "
-                             "1250 TFLOP/s is its own ceiling"}}, ensure_ascii=False))
+                             "1250 TFLOP/s is its own ceiling"}, **extra}, ensure_ascii=False))
     return 0
+
+
+def projection_cpu_baseline(calls, n, seconds, layer_flops, sample_rows=16):
+    """linear_f32 of pvlc-cpu-ref restated in C (oracle/), single thread, on the same inputs (fp16 weights
+    widened to f32): the first sample_rows rows of each of the layer's four projections, repeated for a bounded
+    time and scaled to N rows; the GPU's rows are checked against it."""
+    import oracle as O
+
+    host = []
+    for name, out_w, in_w, x, w, b, y, ws, wsb in calls:
+        host.append((x[:sample_rows * in_w].cpu().numpy(), w.float().cpu().numpy(), b.cpu().numpy(), in_w, out_w,
+                     y[:sample_rows * out_w].cpu().numpy()))
+    elapsed, reps, max_rel = 0.0, 0, 0.0
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or reps == 0:
+        for xs, wf, bs, in_w, out_w, gpu in host:
+            t0 = time.perf_counter()
+            want = O.linear_f32(xs, sample_rows, in_w, wf, bs, out_w)
+            elapsed += time.perf_counter() - t0
+            if reps == 0:
+                max_rel = max(max_rel, float(np.max(np.abs(gpu - want) / np.maximum(np.abs(want), 1e-3))))
+        reps += 1
+    per_layer = elapsed / reps * (n / sample_rows)
+    return {"value": round(per_layer * 1e6, 1), "unit": "µs/layer", "cores": 1, "kind": "port",
+            "tflops": round(layer_flops / per_layer / 1e12, 6),
+            "sample": f"{reps} x first {sample_rows} rows of the 4 projections, scaled to N={n} ({elapsed:.1f} s)",
+            "gpu_vs_cpu_max_rel": max_rel}
 
 
 def gemv_cpu_baseline(calls, logits, seconds, step_bytes):

@@ -42,6 +42,7 @@ constexpr int kQueryBlock = 16;  // query tokens per workgroup
 constexpr int kKeyStep = 64;     // keys per softmax step (4 cache blocks)
 constexpr int kStepTiles = kKeyStep / 16;
 constexpr int kWaves = 4;        // each wave: 2 of the 8 heads of the group
+constexpr float kLazyRescaleLog2 = 8.0f;  // softmax reference moves only past 2^8
 
 struct PrefillParams {
     uint32_t tokens;
@@ -478,16 +479,26 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
         __builtin_amdgcn_s_setprio(0);
         if (more) {
             if (mask_next) apply_mask(s_begin + i + 1, xn);
+            // Lazy rescale: m_run is the exponent reference of the column,
+            // and it moves (with O and the row sums rescaled) only when the
+            // column's maximum exceeds it by more than kLazyRescaleLog2;
+            // until then every weight 2^(s - m_run) stays below 2^8, exact
+            // in fp16 and far from f32 overflow in the sums.  O / l is the
+            // same quotient whatever the reference, and the split merge
+            // takes m_run as the reference its part used.
             float m_new[2];
             column_max(xn, m_run, m_new);
-            bool moved = false;
+            bool far = false;
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                alpha[ct] = __builtin_amdgcn_exp2f((m_run[ct] - m_new[ct]) * scale);
-                moved |= m_new[ct] != m_run[ct];
-                m_run[ct] = m_new[ct];
+            for (int ct = 0; ct < 2; ++ct) far |= (m_new[ct] - m_run[ct]) * scale > kLazyRescaleLog2;
+            rescale = __any(far);
+            if (rescale) {  // uniform
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    alpha[ct] = __builtin_amdgcn_exp2f((m_run[ct] - m_new[ct]) * scale);
+                    m_run[ct] = m_new[ct];
+                }
             }
-            rescale = __any(moved);
         }
         __syncthreads();  // waits for this wave's loads into LDS, then for every wave
     };

@@ -24,11 +24,12 @@ def prefill_workspace(n):
     return ws, nbytes
 
 
-def run_prefill(n, seed, table=None, num_blocks=None, scale=0.5, rope=True, with_scratch=False, workspace=None):
+def run_prefill(n, seed, table=None, num_blocks=None, scale=0.5, rope=True, with_scratch=False, workspace=None,
+                q=None, k=None):
     import torch
     nb = num_blocks or (n + 15) // 16
-    q = f16_bits(seed, n * 2048, scale)
-    k = f16_bits(seed + 1, n * W, scale)
+    q = f16_bits(seed, n * 2048, scale) if q is None else q
+    k = f16_bits(seed + 1, n * W, scale) if k is None else k
     v = f16_bits(seed + 2, n * W, scale)
     cos, sin = pvlc.rope_table(BASE, n)
     d_k = torch.zeros(nb * 16 * W, dtype=torch.int16, device="cuda")
@@ -133,3 +134,19 @@ def test_split_and_unsplit_schedules_agree_and_the_workspace_is_reusable():
     # every arrival counter is back to zero
     counters = ws[0][:256 * 2].view(torch.int32)
     assert int(counters.abs().sum().item()) == 0
+
+
+@pytest.mark.parametrize("n,split", [(1100, False), (3000, True)])
+def test_scores_rising_along_the_sequence_move_the_softmax_reference(n, split):
+    """Keys whose scores grow by ~41 log2 units along the sequence: the running maximum of every query passes
+    its exponent reference several times (the kernel rescales O and the row sums only when the maximum exceeds
+    the reference by 2^8), in both schedules, against decode over i + 1 keys."""
+    log(f"case: prefill rising scores N={n} split={split}")
+    rng = np.random.default_rng(n)
+    q = O.f32_to_f16((0.25 + 0.01 * rng.standard_normal(n * 2048)).astype(np.float32))
+    c = (10.0 * np.arange(n) / n).astype(np.float32)
+    k = O.f32_to_f16((np.repeat(c, W) * (1.0 + 0.1 * rng.standard_normal(n * W))).astype(np.float32))
+    ws = prefill_workspace(n) if split else None
+    out, qr, kr, vr, scratch, _ = run_prefill(n, seed=n, rope=False, q=q, k=k, workspace=ws)
+    rows = [0, 1, 16, 63, 64, 200, n // 2, n - 65, n - 2, n - 1]
+    sampled_rows_match_decode(out, qr, kr, vr, n, rows, f"rising N={n}")
