@@ -435,9 +435,9 @@ def bench_gemv(args):
     step_bytes = sum(gemv_bytes(r, c) for _, _, _, r, c in separate)
     fused_bytes = sum(gemv_bytes(r, c) for _, _, _, r, c in fused)
 
-    def step(calls):
+    def step(calls, st=stream):
         for w_, x_, o_, r_, c_ in calls:
-            pvlc.gemv_f16(w_, x_, o_, r_, c_, stream)
+            pvlc.gemv_f16(w_, x_, o_, r_, c_, st)
 
     torch.cuda.synchronize()
     if args.profile_steps:
@@ -458,8 +458,13 @@ def bench_gemv(args):
         step(separate)
         step(fused)
     steps = min(args.steps, 100)
-    ms = _timed_launches(torch, stream, steps, lambda i: step(separate))
-    ms_fused = _timed_launches(torch, stream, steps, lambda i: step(fused))
+    ms_eager = _timed_launches(torch, stream, steps, lambda i: step(separate))
+    ms_fused_eager = _timed_launches(torch, stream, steps, lambda i: step(fused))
+    # The decode loop captures its launches once and replays them: the same kernels and arguments as the eager
+    # launches, replayed from a HIP graph (the first replay is checked against the eager outputs bit for bit).
+    graph_sep, graph_fused = _gemv_graph(torch, step, separate), _gemv_graph(torch, step, fused)
+    ms = _timed_launches(torch, stream, steps, lambda i: graph_sep.replay())
+    ms_fused = _timed_launches(torch, stream, steps, lambda i: graph_fused.replay())
     gbps = step_bytes / (ms * 1e-3) / 1e9
     gbps_fused = fused_bytes / (ms_fused * 1e-3) / 1e9
 
@@ -489,12 +494,14 @@ def bench_gemv(args):
         "data": "synthetic N(0,1)*0.02 fp16 weights, N(0,1) f32 vectors, seeded",
         "config": {"workload": "one decoder token step's weight GEMVs: 18 x (q 2048x1024, k/v 256x1024, o 1024x2048, "
                                "gate/up 3072x1024, down 1024x3072) + LM head 103424x1024, each layer its own weights",
-                   "launches_per_step": len(separate)},
+                   "launches_per_step": len(separate), "launch": "HIP graph replay of the step's launches"},
+        "eager_us": round(ms_eager * 1e3, 2),
         "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                      "algorithmic_bytes_per_step": step_bytes},
         "rows_concatenated": {"launches_per_step": len(fused), "us": round(ms_fused * 1e3, 2),
+                              "eager_us": round(ms_fused_eager * 1e3, 2),
                               "gbps": round(gbps_fused, 1), "pct_hbm_peak": round(100 * gbps_fused / HBM_PEAK_GBPS, 2)},
         "per_shape_hbm": shapes,
         "lm_head_top1": top1,
@@ -503,6 +510,27 @@ def bench_gemv(args):
         result["cpu_baseline"] = gemv_cpu_baseline(separate, logits, args.cpu_seconds, step_bytes)
     print(json.dumps(result, ensure_ascii=False))
     return 0
+
+
+def _gemv_graph(torch, step, calls):
+    """Capture step(calls) into a HIP graph on a side stream; check one replay against eager launches."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(calls, side)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    want = [o_.clone() for _, _, o_, _, _ in calls]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(calls, torch.cuda.current_stream())
+    for _, _, o_, _, _ in calls:
+        o_.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    if not all(torch.equal(w_, o_) for w_, (_, _, o_, _, _) in zip(want, calls)):
+        raise RuntimeError("GEMV step replayed from a HIP graph differs from the eager launches")
+    return graph
 
 
 def _bench_top1(pvlc, torch, stream, heads, hidden, logits, rows, columns, k):
