@@ -302,6 +302,20 @@ void pvlc_hip_kv_session_fail_next_step_after_submit(pvlc_hip_kv_session *sessio
 pvlc_hip_status pvlc_hip_rope_table_f32(float base, uint32_t rotary_dim, uint32_t rows, float *cos_out,
                                         float *sin_out);
 
+/* Multimodal RoPE tables: the section selection of decoder_mrope_f32 and
+ * decoder_prefill_mrope_f32 (pvlc-wgsl lib.rs:1185-1234, :1334-1380;
+ * apply_multimodal_rope_f32, cpu-ref lib.rs:562-672) applied to raw cos/sin
+ * tables [3][capacity][128] (temporal, height, width) with sections
+ * (section_t, section_h, section_w) of the 64 frequency pairs (16, 24, 24 in
+ * the shaders), giving the [capacity][64] tables the decode and prefill
+ * entry points read; slot p of the tables is selected by the token's position
+ * p.  Raw rows must repeat their first half (the device rotation reads one
+ * cos/sin per pair); rows that do not are rejected (InvalidRotaryDimension),
+ * as are non-finite values (NonFiniteInput).  Host only. */
+pvlc_hip_status pvlc_hip_mrope_table_f32(const float *raw_cos, const float *raw_sin, uint32_t capacity,
+                                         uint32_t section_t, uint32_t section_h, uint32_t section_w, float *cos_out,
+                                         float *sin_out);
+
 /* IEEE binary16 round-to-nearest-even conversion on the host (the rounding the
  * kernels apply to every value they store). */
 void pvlc_hip_f32_to_f16_host(const float *in, uint16_t *out, size_t n);

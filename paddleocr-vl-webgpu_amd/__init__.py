@@ -197,6 +197,7 @@ SIGNATURES = {
     "pvlc_hip_kv_session_destroy": ([_VP], None),
     "pvlc_hip_kv_session_fail_next_step_after_submit": ([_VP], None),
     "pvlc_hip_rope_table_f32": ([ctypes.c_float, _U32, _U32, _F, _F], ctypes.c_int32),
+    "pvlc_hip_mrope_table_f32": ([_F, _F, _U32, _U32, _U32, _U32, _F, _F], ctypes.c_int32),
     "pvlc_hip_f32_to_f16_host": ([_F, _U16, _SZ], None),
     "pvlc_hip_f16_to_f32_host": ([_U16, _F, _SZ], None),
     "pvlc_hip_paged_decode_partition": ([_U32, _U32], _U32),
@@ -490,6 +491,21 @@ def rope_table(base: float, rows: int, rotary_dim: int = HEAD_DIM) -> tuple[np.n
     sin = np.zeros(rows * half, np.float32)
     _check(lib.pvlc_hip_rope_table_f32(ctypes.c_float(base), rotary_dim, rows, _fp(cos), _fp(sin)))
     return cos.reshape(rows, half), sin.reshape(rows, half)
+
+
+def mrope_table(raw_cos, raw_sin, capacity: int, sections=(16, 24, 24)) -> tuple[np.ndarray, np.ndarray]:
+    """[capacity][64] cos/sin tables from raw M-RoPE tables [3][capacity][128] (decoder_mrope_f32's section
+    selection, pvlc-wgsl lib.rs:1185-1234)."""
+    rc = np.ascontiguousarray(raw_cos, dtype=np.float32).ravel()
+    rs = np.ascontiguousarray(raw_sin, dtype=np.float32).ravel()
+    if rc.size != 3 * capacity * HEAD_DIM or rs.size != rc.size:
+        raise PvlcHipError(0x300 | 2, "raw M-RoPE tables must hold 3 x capacity x 128 values")
+    half = HEAD_DIM // 2
+    cos = np.zeros(capacity * half, np.float32)
+    sin = np.zeros(capacity * half, np.float32)
+    _check(lib.pvlc_hip_mrope_table_f32(_fp(rc), _fp(rs), capacity, sections[0], sections[1], sections[2], _fp(cos),
+                                        _fp(sin)))
+    return cos.reshape(capacity, half), sin.reshape(capacity, half)
 
 
 def f32_to_f16(values) -> np.ndarray:

@@ -560,4 +560,38 @@ pvlc_hip_status pvlc_hip_rope_table_f32(float base, uint32_t rotary_dim, uint32_
     return ok();
 }
 
+pvlc_hip_status pvlc_hip_mrope_table_f32(const float *raw_cos, const float *raw_sin, uint32_t capacity,
+                                         uint32_t section_t, uint32_t section_h, uint32_t section_w, float *cos_out,
+                                         float *sin_out) {
+    // Section selection of apply_multimodal_rope_f32 (cpu-ref lib.rs:562-672) and decoder_mrope_f32 /
+    // decoder_prefill_mrope_f32 (wgsl lib.rs:1185-1234, 1334-1380): frequency pair f of a slot reads axis
+    // 0 (temporal) for f < section_t, 1 (height) below section_t + section_h, else 2 (width); the raw tables
+    // are [3][capacity][128] and the device rotation reads one cos/sin per pair, so every raw row must
+    // repeat its first half (as cat(freqs, freqs) tables do).
+    constexpr uint32_t kDim = 128, kHalf = 64;
+    if (!raw_cos || !raw_sin || !cos_out || !sin_out)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "M-RoPE table pointers are NULL");
+    if (capacity == 0 || section_t == 0 || section_h == 0 || section_w == 0)
+        return invalid(PVLC_HIP_INV_ZERO_DIMENSION, "M-RoPE capacity and sections must be nonzero");
+    if (static_cast<uint64_t>(section_t) + section_h + section_w != kHalf)
+        return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION, "M-RoPE sections must sum to head_dim / 2 = 64");
+    const size_t n = static_cast<size_t>(3) * capacity * kDim;
+    for (size_t i = 0; i < n; ++i)
+        if (!std::isfinite(raw_cos[i]) || !std::isfinite(raw_sin[i]))
+            return invalid(PVLC_HIP_INV_NON_FINITE_INPUT, "M-RoPE tables contain NaN or infinity");
+    for (size_t row = 0; row < static_cast<size_t>(3) * capacity; ++row)
+        if (std::memcmp(raw_cos + row * kDim, raw_cos + row * kDim + kHalf, kHalf * sizeof(float)) != 0 ||
+            std::memcmp(raw_sin + row * kDim, raw_sin + row * kDim + kHalf, kHalf * sizeof(float)) != 0)
+            return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION,
+                           "M-RoPE table row " + std::to_string(row) + " does not repeat its first half");
+    for (uint32_t slot = 0; slot < capacity; ++slot)
+        for (uint32_t f = 0; f < kHalf; ++f) {
+            const uint32_t axis = f < section_t ? 0u : (f < section_t + section_h ? 1u : 2u);
+            const size_t src = (static_cast<size_t>(axis) * capacity + slot) * kDim + f;
+            cos_out[static_cast<size_t>(slot) * kHalf + f] = raw_cos[src];
+            sin_out[static_cast<size_t>(slot) * kHalf + f] = raw_sin[src];
+        }
+    return ok();
+}
+
 }  // extern "C"
