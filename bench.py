@@ -38,6 +38,7 @@ sys.path.insert(0, REPO)
 LAYERS = 18
 CONTEXT = 2048  # rows attended after the append
 CAPACITY = 2304  # 1280 + 1024 (config 2's last context)
+SWEEP_PREFIX, SWEEP_STEPS = 1280, 1024  # config 2's sweep: T = 1281..2304
 ROPE_BASE = 500000.0
 HBM_PEAK_GBPS = 8000.0
 W = 256
@@ -225,6 +226,27 @@ def main() -> int:
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(host_q, host_k, host_v, host_nk, host_nv, cos, sin, args.cpu_seconds,
                                               step_bytes, replicas[0]["keep"][5])
+    # The config-2 sweep: prefix 1280, 1024 steps, T = 1281..2304 (step i appends row 1280 + i and attends over
+    # 1281 + i rows), rotating the replicas as above.  Run after the CPU baseline: its appends overwrite rows of
+    # replica 0.
+    sweep = []
+    for i in range(SWEEP_STEPS):
+        kp, vp, q, nk, nv, out = replicas[i % len(replicas)]["keep"]
+        sweep.append(pvlc.paged_decode_args(num_seqs=LAYERS, num_blocks=LAYERS * nb_per, max_blocks_per_seq=nb_per,
+                                            key_cache=kp, value_cache=vp, query=q, new_key=nk, new_value=nv,
+                                            out=out, workspace=ws, workspace_bytes=wsb, max_context=CAPACITY,
+                                            uniform_cache_len=SWEEP_PREFIX + i, rope_cos=d_cos, rope_sin=d_sin,
+                                            rope_rows=CAPACITY, partition_tokens=args.partition))
+    for a in sweep[:len(replicas)]:
+        pvlc.paged_decode_f16(a, stream)
+    sweep_ms = _timed_launches(torch, stream, len(sweep), lambda i: pvlc.paged_decode_f16(sweep[i], stream))
+    sweep_bytes = sum(LAYERS * algorithmic_bytes(SWEEP_PREFIX + 1 + i) for i in range(SWEEP_STEPS))
+    sweep_gbps = sweep_bytes / (sweep_ms * 1e-3 * SWEEP_STEPS) / 1e9
+    result["config2_sweep"] = {"steps": SWEEP_STEPS, "context": f"{SWEEP_PREFIX + 1}..{SWEEP_PREFIX + SWEEP_STEPS}",
+                               "mean_us_per_step": round(sweep_ms * 1e3, 3), "gbps": round(sweep_gbps, 1),
+                               "pct_hbm_peak": round(100 * sweep_gbps / HBM_PEAK_GBPS, 2),
+                               "algorithmic_bytes": sweep_bytes,
+                               "device_error_word": pvlc.workspace_error(ws, wsb, stream)}
     print(json.dumps(result, ensure_ascii=False))
     return 0
 
