@@ -75,6 +75,15 @@ def test_projection_at_prefill_size_sampled_rows():
     check(rows, k, n, got, wf, x, b, "4096x1024x2560", oracle_rows=[0, 1, 127, 128, 2047, 3000, 4094, 4095])
 
 
+def test_wide_output_and_ragged_rows_sampled():
+    """A wide output (7940 columns, not a multiple of the 128-column tile) over ragged rows (2049: a last row tile
+    of one row), sampled rows against the f64 bound."""
+    rows, k, n = 2049, 1024, 7940
+    log("case: projection 2049x1024x7940 (wide tiles, sampled rows)")
+    got, wf, x, b = run_projection(rows, k, n, seed=2049)
+    check(rows, k, n, got, wf, x, b, "2049x1024x7940", oracle_rows=[0, 1, 127, 128, 1023, 2047, 2048])
+
+
 def test_rows_far_outside_the_fp16_range_keep_f32_accuracy():
     rows, k, n = 6, 1024, 64
     rng = np.random.default_rng(9)
