@@ -402,20 +402,24 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
             for (int e = 0; e < 8; ++e) pa[ct][j][e] = to_h(__builtin_amdgcn_exp2f(__builtin_fmaf(x[ct][j][e], scale, -ms[ct])));
     };
     // O += P.V over pair j, and the row sums += P.1 (exactly the rounded weights).
+    // The pair's 8 value fragments are read from LDS before its MFMAs.
     auto pv_mfma = [&](const uint16_t *vl, int j, const half8_t (&pa)[2][2]) {
+        half8_t vf[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            vf[c] = *reinterpret_cast<const half8_t *>(vl + lds_value_offset(j, kg >> 1, kg & 1, c * 16 + row));
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            const half8_t vf = *reinterpret_cast<const half8_t *>(vl + lds_value_offset(j, kg >> 1, kg & 1, c * 16 + row));
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) o[ct][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ct][j], vf, o[ct][c], 0, 0, 0);
+            for (int ct = 0; ct < 2; ++ct) o[ct][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ct][j], vf[c], o[ct][c], 0, 0, 0);
         }
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) o[ct][8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ct][j], ones, o[ct][8], 0, 0, 0);
     };
 
     // Software pipeline: while the score MFMAs of step i+1 run, the VALU
-    // rescales O and exponentiates half of step i; while P.V of step i runs,
-    // it exponentiates the other half, then masks step i+1 and takes its max.
+    // exponentiates step i (and rescales O when the reference moved); while
+    // P.V of step i runs, it masks step i+1 and takes its max.
     // K stays one step ahead of V through LDS: step i (parity i & 1) reads
     // K(i+1) from sk[(i+1)&1] and V(i) from sv[i&1], and at its start loads
     // K(i+2) into sk[i&1] and V(i+1) into sv[(i+1)&1] (both freed by step
@@ -466,15 +470,12 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
         // scores of step i+1 | P of step i, pair 0
         if (more) scores(k_read, xn);
         probs(xc, ms, 0, pa);
-        // P.V of pair 0 | P of pair 1.  The P.V MFMAs run at raised wave
-        // priority, so the SIMD's other wave fills the gaps with its VALU work
-        // (measured 4-6% faster than equal priorities).
+        probs(xc, ms, 1, pa);
+        // P.V of both pairs | mask and max of step i+1.  The P.V MFMAs run at
+        // raised wave priority, so the SIMD's other wave fills the gaps with
+        // its VALU work.
         __builtin_amdgcn_s_setprio(1);
         pv_mfma(v_read, 0, pa);
-        __builtin_amdgcn_s_setprio(0);
-        probs(xc, ms, 1, pa);
-        // P.V of pair 1 | mask and max of step i+1
-        __builtin_amdgcn_s_setprio(1);
         pv_mfma(v_read, 1, pa);
         __builtin_amdgcn_s_setprio(0);
         if (more) {
