@@ -343,14 +343,61 @@ def bench_batched(args):
     total_t = int(lens.sum())
     step_bytes = 1024 * total_t + num_seqs * 10240
     gbps = step_bytes / (ms * 1e-3) / 1e9
-    print(json.dumps({"metric": "paged batched decode step µs + achieved HBM GB/s", "config": {
+    result = {"metric": "paged batched decode step µs + achieved HBM GB/s", "config": {
         "workload": label, "num_seqs": num_seqs, "sum_T": total_t, "max_T": max_context, "cache_replicas": reps,
         "partition_tokens": part or pvlc.decode_partition(num_seqs, max_context)},
         "value": round(ms * 1e3, 2), "unit": "µs/step", "steps": args.steps, "warmup": args.warmup,
         "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
-        "algorithmic_bytes": step_bytes, "device_error_word": pvlc.workspace_error(ws, wsb, stream)},
-        ensure_ascii=False))
+        "algorithmic_bytes": step_bytes, "device_error_word": pvlc.workspace_error(ws, wsb, stream),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
+    if not args.no_cpu:
+        # replica 0 again, so `out` and its cache hold the step the CPU recomputes
+        pvlc.paged_decode_f16(launches[0], stream)
+        torch.cuda.synchronize()
+        result["cpu_baseline"] = batched_cpu_baseline(pvlc, torch, planes[0], d_tables, num_blocks, lens, q, out,
+                                                      args.cpu_seconds, step_bytes)
+    print(json.dumps(result, ensure_ascii=False))
     return 0
+
+
+def batched_cpu_baseline(pvlc, torch, plane, d_tables, num_blocks, lens, q, out, seconds, step_bytes, sample=6):
+    """decode_gqa_f32 of pvlc-cpu-ref restated in C (oracle/), single thread, on a sample of the batch's
+    sequences (spread over the length distribution) after the step: their rows are unpacked from the paged
+    cache (the appended rotated key included), the oracle attends the step's queries over them, and the time is
+    scaled by the batch's total rows to one step; the sampled outputs are compared with the GPU's."""
+    import oracle as O
+
+    order = np.argsort(lens)
+    picks = order[np.linspace(0, len(lens) - 1, sample).astype(int)]
+    host_q = q.cpu().numpy().view(np.uint16)
+    host_out = O.f16_to_f32(out.cpu().numpy().view(np.uint16))
+    rows = []
+    for s in picks:
+        t = int(lens[s])
+        kr = torch.empty(t * W, dtype=torch.float16, device=q.device)
+        vr = torch.empty_like(kr)
+        pvlc.kv_unpack_f16(plane[0], plane[1], t, kr, vr, num_blocks, block_table=d_tables[s])
+        torch.cuda.synchronize()
+        rows.append((s, t, O.f16_to_f32(host_q[s * 2048:(s + 1) * 2048]),
+                     O.f16_to_f32(kr.cpu().numpy().view(np.uint16)), O.f16_to_f32(vr.cpu().numpy().view(np.uint16))))
+    elapsed, reps, max_abs = 0.0, 0, 0.0
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or reps == 0:
+        for s, t, qs, ks, vs in rows:
+            t0 = time.perf_counter()
+            want = O.decode_gqa_f32(qs, ks, vs, t, 16, 2, 128)
+            elapsed += time.perf_counter() - t0
+            if reps == 0:
+                max_abs = max(max_abs, float(np.abs(host_out[s * 2048:(s + 1) * 2048] - want).max()))
+        reps += 1
+    sample_rows = sum(t for _, t, _, _, _ in rows)
+    per_step = elapsed / reps * (int(lens.sum()) / sample_rows)
+    return {"value": round(per_step * 1e6, 1), "unit": "µs/step", "cores": 1, "kind": "port",
+            "gbps": round(step_bytes / per_step / 1e9, 3),
+            "sample": f"{reps} x decode_gqa_f32 of {len(rows)} sequences ({sample_rows} rows), scaled by the "
+                      f"batch's {int(lens.sum())} rows ({elapsed:.1f} s)",
+            "gpu_vs_cpu_max_abs": max_abs}
 
 
 def bench_prefill(args):
@@ -389,15 +436,53 @@ def bench_prefill(args):
     ms = _timed_launches(torch, stream, args.steps, call)
     flops = 16 * (n * (n + 1) // 2) * 512
     tflops = flops / (ms * 1e-3) / 1e12
-    print(json.dumps({"metric": "causal prefill µs + MFMA TFLOP/s (% fp16 dense peak)", "config": {
+    result = {"metric": "causal prefill µs + MFMA TFLOP/s (% fp16 dense peak)", "config": {
         "workload": "config 4: N=4096, 16q/2kv d128 fp16, x0.5, rotary on Q,K, rows written to the paged cache",
         "workspace_bytes": wsb},
         "value": round(ms * 1e3, 2), "unit": "µs/call", "steps": args.steps, "warmup": args.warmup,
         "achieved_tflops": round(tflops, 1), "pct_mfma_peak": round(100 * tflops / 2500.0, 2),
         "algorithmic_flops": flops, "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0,
-                                                 "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4)}},
-        ensure_ascii=False))
+                                                 "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4)}}
+    if not args.no_cpu:
+        result["cpu_baseline"] = prefill_cpu_baseline(pvlc, torch, n, nb, q, kp, vp, out, args.cpu_seconds, flops)
+    print(json.dumps(result, ensure_ascii=False))
     return 0
+
+
+def prefill_cpu_baseline(pvlc, torch, n, nb, q, kp, vp, out, seconds, flops, sample=16):
+    """causal_gqa_f32 of pvlc-cpu-ref restated in C (oracle/), single thread, on a sample of query rows: row i of
+    the causal attention is the decode over keys 0..i (the reference's own identity, decoder_decode_contract.rs:
+    888-1047), on the rotated keys and values the GPU wrote to the cache and the oracle's rotation of the
+    query; the time is scaled by the N(N+1)/2 attended rows and the sampled rows compared with the GPU's."""
+    import oracle as O
+
+    kr = torch.empty(n * W, dtype=torch.float16, device=q.device)
+    vr = torch.empty_like(kr)
+    pvlc.kv_unpack_f16(kp, vp, n, kr, vr, nb)
+    torch.cuda.synchronize()
+    keys = O.f16_to_f32(kr.cpu().numpy().view(np.uint16))
+    values = O.f16_to_f32(vr.cpu().numpy().view(np.uint16))
+    host_q = O.f16_to_f32(q.cpu().numpy().view(np.uint16))
+    host_out = O.f16_to_f32(out.cpu().numpy().view(np.uint16))
+    picks = np.linspace(0, n - 1, sample).astype(int)
+    qrot = {i: O.rope_neox_f32(host_q[i * 2048:(i + 1) * 2048], 16, 128, 128, [i] * 16, ROPE_BASE) for i in picks}
+    elapsed, reps, max_abs = 0.0, 0, 0.0
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or reps == 0:
+        for i in picks:
+            t0 = time.perf_counter()
+            want = O.decode_gqa_f32(qrot[i], keys[:(i + 1) * W], values[:(i + 1) * W], i + 1, 16, 2, 128)
+            elapsed += time.perf_counter() - t0
+            if reps == 0:
+                max_abs = max(max_abs, float(np.abs(host_out[i * 2048:(i + 1) * 2048] - want).max()))
+        reps += 1
+    sampled = int(sum(i + 1 for i in picks))
+    per_call = elapsed / reps * ((n * (n + 1) // 2) / sampled)
+    return {"value": round(per_call * 1e6, 1), "unit": "µs/call", "cores": 1, "kind": "port",
+            "tflops": round(flops / per_call / 1e12, 6),
+            "sample": f"{reps} x {sample} query rows (decode over keys 0..i, {sampled} attended rows), scaled to "
+                      f"N(N+1)/2 = {n * (n + 1) // 2} ({elapsed:.1f} s)",
+            "gpu_vs_cpu_max_abs": max_abs}
 
 
 # Decoder projections of one layer, rows x columns (gemv_tiled_plan_contract.rs and
