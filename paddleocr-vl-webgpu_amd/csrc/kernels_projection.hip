@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_kernel(
     // XCDs, so workgroup b runs on XCD b % 8; the permutation below gives XCD
     // x a contiguous range of tiles in row-major order (whole bands of output
     // rows), and the L2 of that XCD serves every column tile of its rows.
-    const uint32_t n_tiles = (n_width + kTileN - 1) / kTileN;
+    const uint32_t n_tiles = n_width / kTileN + (n_width % kTileN != 0);
     const uint32_t total = gridDim.x, xcd = blockIdx.x % kXcds, idx = blockIdx.x / kXcds;
     const uint32_t q = total / kXcds, r = total % kXcds;
     const uint32_t tile = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
@@ -293,7 +293,7 @@ int launch_linear_projection_f16(const float *input, const uint16_t *weight, con
     default: hipLaunchKernelGGL(projection_split_kernel<0>, split_grid, dim3(kSplitThreads), 0, st, input, rows, k_width, ws.tiles, ws.exponents); break;
     }
     if (hipError_t e = hipGetLastError()) return static_cast<int>(e);
-    const uint32_t tiles = ((n_width + kTileN - 1) / kTileN) * m_tiles;
+    const uint32_t tiles = (n_width / kTileN + (n_width % kTileN != 0)) * m_tiles;  // < 2^24 (checked by the caller)
     hipLaunchKernelGGL(projection_gemm_kernel, dim3(tiles), dim3(kGemmThreads), 0, st, ws.tiles, ws.exponents, weight,
                        bias, out, rows, k_width, n_width);
     return static_cast<int>(hipGetLastError());

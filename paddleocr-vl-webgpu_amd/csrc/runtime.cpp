@@ -546,8 +546,10 @@ pvlc_hip_status pvlc_hip_linear_projection_f16(const float *input, const uint16_
                        "projection geometry must be positive with widths a multiple of 4");
     if (input_width % 32 != 0)
         return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "device projection needs input_width a multiple of 32");
-    if (rows > 65535u * 128u)
-        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "projection rows exceed the grid");
+    // One workgroup of 256 threads per 128 x 128 output tile: the grid holds fewer than 2^32 threads.
+    const uint64_t out_tiles = (static_cast<uint64_t>(rows) + 127) / 128 * ((static_cast<uint64_t>(output_width) + 127) / 128);
+    if (rows > 65535u * 128u || out_tiles >= (1u << 24))
+        return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY, "projection rows or output tiles exceed the grid");
     for (const void *ptr : {static_cast<const void *>(input), static_cast<const void *>(weight),
                             static_cast<const void *>(output)})
         if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0)

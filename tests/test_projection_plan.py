@@ -125,6 +125,7 @@ def test_device_projection_validates_before_touching_the_gpu():
         ((fake, fake, fake, fake, 64, 1000, 256, fake, ws), "InvalidDecoderGeometry"),  # width not a multiple of 32
         ((fake, fake, fake, fake, 64, 1024, 6, fake, ws), "InvalidDecoderGeometry"),    # not a multiple of 4
         ((fake, fake, fake, fake, 0, 1024, 256, fake, ws), "InvalidDecoderGeometry"),
+        ((fake, fake, fake, fake, 64 * 128, 1024, 2**32 - 4, fake, ws), "InvalidDecoderGeometry"),  # tiles > 2^24
         ((fake, fake, fake, fake, 64, 1024, 256, fake, ws - 4), "LengthMismatch"),
         ((fake, fake, fake, fake, 64, 1024, 256, fake + 16, ws), "LengthMismatch"),    # workspace alignment
         ((fake + 8, fake, fake, fake, 64, 1024, 256, fake, ws), "LengthMismatch"),     # input alignment
