@@ -351,6 +351,10 @@ def bench_batched(args):
         "algorithmic_bytes": step_bytes, "device_error_word": pvlc.workspace_error(ws, wsb, stream),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
+    if not part:
+        # An automatic streaming launch records the partition it settled on after the error word.
+        words = ws[:16].cpu().numpy().view(np.uint32)
+        result["config"]["partition_chosen_on_device"] = int(words[1])
     if not args.no_cpu:
         # replica 0 again, so `out` and its cache hold the step the CPU recomputes
         pvlc.paged_decode_f16(launches[0], stream)

@@ -58,10 +58,13 @@ struct DecodeParams {
     uint32_t rotate_query;
     uint32_t partition_tokens;
     uint32_t max_parts;
-    float *part_o;      // [seq][kv head][part][8 heads][128]
-    float *part_ml;     // [seq][kv head][part][8 heads][2]: max (log2 units), sum
+    uint32_t part_stride;  // partial slots per (seq, kv head): max_parts rounded up to odd
+    float *part_o;      // [seq][kv head][part_stride][8 heads][128]
+    float *part_ml;     // [seq][kv head][part_stride][8 heads][2]: max (log2 units), sum
     uint32_t *counters; // [seq][kv head]
     uint32_t *error_word;
+    uint32_t *partition_word;  // streaming, automatic partition: the one used (else null)
+    uint32_t compute_units;    // streaming: compute units of the device
     float scale_log2;   // log2(e)/sqrt(128)
 };
 
@@ -419,7 +422,7 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
         return;
     }
 
-    const size_t unit = (static_cast<size_t>(s) * kKvHeads + g) * p.max_parts;
+    const size_t unit = (static_cast<size_t>(s) * kKvHeads + g) * p.part_stride;
     float *part_o = p.part_o + (unit + part) * (kGroup * kHeadDim);
     float *part_ml = p.part_ml + (unit + part) * (2 * kGroup);  // [head][max, sum]
     if constexpr (DEFER_MERGE) {
@@ -577,6 +580,9 @@ __device__ inline int workgroup_exclusive_scan(int v, int *sm_wave_sums, int *to
     return before + x - v;
 }
 
+// Partition lengths an automatic streaming launch chooses from: P0 + c P0/4.
+constexpr int kPartitionChoices = 5;
+
 // Persistent grid for ragged lengths and long contexts: every workgroup
 // reads the cache lengths (and positions) once into LDS, numbers the (sequence, partition,
 // kv head) items that hold rows, and walks items blockIdx.x,
@@ -590,18 +596,68 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
     __shared__ int sm_len[kMaxRaggedSeqs];        // cache length, -1 if invalid
     __shared__ int sm_pos[kMaxRaggedSeqs];        // rotary position of the appended row
     __shared__ int sm_wave_sums[WAVES];
-    const int P = static_cast<int>(p.partition_tokens);
+    __shared__ int sm_counts[kPartitionChoices][WAVES];
     const int n = static_cast<int>(num_seqs);
     const int per = (n + kThreads - 1) / kThreads;
     const int i0 = static_cast<int>(threadIdx.x) * per;
-    int local = 0;
+    // Validity is judged against the partition the host planned with.
+    const int P0 = static_cast<int>(p.partition_tokens);
+    const int step = max(16, (P0 / 4) & ~15);
+    int counts[kPartitionChoices] = {};
     for (int i = i0; i < min(i0 + per, n); ++i) {
         const int64_t len =
             checked_cache_len(p, p.cache_lens ? p.cache_lens[i] : static_cast<int64_t>(p.uniform_cache_len));
         if (len < 0 && blockIdx.x == 0) atomicOr(p.error_word, 1u);
-        const int parts = len < 0 ? 0 : static_cast<int>((len + P) / P);  // ceil((len + 1) / P)
         sm_len[i] = static_cast<int>(len);
         sm_pos[i] = p.positions ? p.positions[i] : static_cast<int>(len);
+        if (p.partition_word) {
+#pragma unroll
+            for (int c = 0; c < kPartitionChoices; ++c) {
+                const int pc = P0 + c * step;
+                counts[c] += len < 0 ? 0 : static_cast<int>((len + pc) / pc);
+            }
+        }
+    }
+    // Automatic partition.  Item k runs on workgroup k mod grid, and the
+    // grid fills every compute unit before it doubles up, so item k lands on
+    // unit k mod units: a unit streams ceil(items / units) items one after the
+    // other at the per-unit HBM rate.  Take the first of P0, P0 + P0/4, ...,
+    // 2 P0 with the least ceil(items / units) * P (every workgroup computes
+    // the same counts from the same lengths).
+    int P = P0;
+    if (p.partition_word) {
+        const int wave = threadIdx.x >> 6;
+#pragma unroll
+        for (int c = 0; c < kPartitionChoices; ++c) {
+            int v = counts[c];
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+            if ((threadIdx.x & 63) == 0) sm_counts[c][wave] = v;
+        }
+        __syncthreads();
+        const uint32_t units = max(1u, p.compute_units);
+        uint64_t best = ~0ull;
+        for (int c = 0; c < kPartitionChoices; ++c) {
+            uint32_t items_c = 0;  // at most 2048 sequences x 64 partitions x 2 heads
+            for (int w = 0; w < WAVES; ++w) items_c += static_cast<uint32_t>(sm_counts[c][w]);
+            items_c *= kKvHeads;
+            const int pc = P0 + c * step;
+            const uint64_t cost = static_cast<uint64_t>((items_c + units - 1) / units) * static_cast<uint32_t>(pc);
+            if (cost < best) {
+                best = cost;
+                P = pc;
+            }
+        }
+        P = __builtin_amdgcn_readfirstlane(P);  // uniform: keep the item arithmetic scalar
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            p.partition_word[0] = static_cast<uint32_t>(P);
+            p.partition_word[1] = static_cast<uint32_t>(units);  // for inspection
+        }
+    }
+    int local = 0;
+    for (int i = i0; i < min(i0 + per, n); ++i) {
+        const int len = sm_len[i];  // written by this thread above
+        const int parts = len < 0 ? 0 : (len + P) / P;  // ceil((len + 1) / P)
         sm_first[i + 1] = parts;
         local += parts;
     }
@@ -628,6 +684,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
         *part_out = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(k - sm_first[lo]));
     };
     const int items = total * static_cast<int>(kKvHeads);
+    DecodeParams q = p;
+    q.partition_tokens = static_cast<uint32_t>(P);
     int item = blockIdx.x;
     if (item >= items) return;
     uint32_t s = 0, part = 0;
@@ -645,7 +703,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
                                                    min(static_cast<int>(part_next + 1) * P, sm_len[s_next] + 1), wave,
                                                    &bad_next);
         }
-        decode_item<WAVES, PAIRS, true>(p, s, static_cast<uint32_t>(item & 1), part, sm_len[s], sm_pos[s], ids, bad);
+        decode_item<WAVES, PAIRS, true>(q, s, static_cast<uint32_t>(item & 1), part, sm_len[s], sm_pos[s], ids, bad);
         if (next >= items) break;
         __syncthreads();  // the next item reuses the workgroup's LDS
         item = next;
@@ -666,12 +724,14 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p)
     const int64_t len = checked_cache_len(
         p, p.cache_lens ? load_const(p.cache_lens, s) : static_cast<int64_t>(p.uniform_cache_len));
     if (len < 0) return;
-    const int P = static_cast<int>(p.partition_tokens);
+    // The ragged kernel wrote the partition it used before this launch began.
+    const int P = static_cast<int>(p.partition_word ? load_const(reinterpret_cast<const int32_t *>(p.partition_word), 0)
+                                                    : p.partition_tokens);
     const int num_parts = static_cast<int>((len + P) / P);
     if (num_parts <= 1) return;
     const int e0 = threadIdx.x * 4;
     const int h = e0 >> 7;
-    const size_t unit = (static_cast<size_t>(s) * kKvHeads + g) * p.max_parts;
+    const size_t unit = (static_cast<size_t>(s) * kKvHeads + g) * p.part_stride;
     const float *all_o = p.part_o + unit * (kGroup * kHeadDim);
     const float *all_ml = p.part_ml + unit * (2 * kGroup);
     constexpr int kBatch = 16;
@@ -717,11 +777,12 @@ __global__ void fill_u32_kernel(uint32_t *dst, size_t words, uint32_t value) {
 
 // Workgroups of `kernel` the current device keeps resident at once (compute
 // units x workgroups per unit), at most max_items; cached per kernel and device.
-uint32_t resident_workgroups(const void *kernel, int threads, uint64_t max_items, int *err) {
+uint32_t resident_workgroups(const void *kernel, int threads, uint64_t max_items, uint32_t *units, int *err) {
     struct Entry {
         const void *kernel;
         int device;
         uint32_t wgs;
+        uint32_t cus;
     };
     static std::mutex mu;
     static std::vector<Entry> cache;
@@ -730,11 +791,14 @@ uint32_t resident_workgroups(const void *kernel, int threads, uint64_t max_items
         *err = static_cast<int>(r);
         return 0;
     }
-    uint32_t wgs = 0;
+    uint32_t wgs = 0, cus_seen = 0;
     {
         std::lock_guard<std::mutex> lock(mu);
         for (const Entry &c : cache)
-            if (c.kernel == kernel && c.device == device) wgs = c.wgs;
+            if (c.kernel == kernel && c.device == device) {
+                wgs = c.wgs;
+                cus_seen = c.cus;
+            }
     }
     if (wgs == 0) {
         int cus = 0, per_cu = 0;
@@ -747,9 +811,11 @@ uint32_t resident_workgroups(const void *kernel, int threads, uint64_t max_items
             return 0;
         }
         wgs = static_cast<uint32_t>(cus * (per_cu > 0 ? per_cu : 1));
+        cus_seen = static_cast<uint32_t>(cus > 0 ? cus : 1);
         std::lock_guard<std::mutex> lock(mu);
-        cache.push_back({kernel, device, wgs});
+        cache.push_back({kernel, device, wgs, cus_seen});
     }
+    *units = cus_seen;
     return static_cast<uint32_t>(max_items < wgs ? (max_items ? max_items : 1) : wgs);
 }
 
@@ -774,10 +840,12 @@ int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
     p.rotate_query = a.rotate_query;
     p.partition_tokens = launch.partition_tokens;
     p.max_parts = launch.max_parts;
+    p.part_stride = launch.part_stride;
     p.part_o = launch.part_o;
     p.part_ml = launch.part_ml;
     p.counters = launch.counters;
     p.error_word = launch.error_word;
+    p.partition_word = launch.partition_word;
     p.scale_log2 = kLog2e / sqrtf(static_cast<float>(kHeadDim));
 
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -789,7 +857,7 @@ int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
 #define PVLC_RAGGED_LAUNCH(W, PR)                                                                                  \
     do {                                                                                                           \
         const uint32_t wgs = resident_workgroups(reinterpret_cast<const void *>(&paged_decode_ragged_kernel<W, PR>), \
-                                                 (W) * 64, max_items, &e);                                         \
+                                                 (W) * 64, max_items, &p.compute_units, &e);                       \
         if (e == 0) {                                                                                              \
             hipLaunchKernelGGL((paged_decode_ragged_kernel<W, PR>), dim3(wgs), dim3((W) * 64), 0, st, p, a.num_seqs); \
             hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(kKvHeads, a.num_seqs), dim3(256), 0, st, p);       \

@@ -84,10 +84,16 @@ struct DecodeLaunch {
     uint32_t pairs;      // pairs of 16-token tiles a wave holds per chunk
     bool streaming;      // persistent kernel + merge kernel (else one workgroup per partition)
     uint32_t max_parts;
+    uint32_t part_stride;
     float *part_o;
     float *part_ml;
     uint32_t *counters;
     uint32_t *error_word;
+    // Streaming regime with an automatic partition: the persistent kernel may
+    // lengthen the partition to fill its last round of items and writes the
+    // partition it used here for the merge kernel, and the compute units it
+    // assumed in the next word (null: partition_tokens as is).
+    uint32_t *partition_word;
 };
 int launch_paged_decode(const DecodeLaunch &launch, void *stream);
 int launch_fill_u32(uint32_t *dst, size_t words, uint32_t value, void *stream);
@@ -203,6 +209,7 @@ int plan_gemv_tiled(uint32_t rows, uint32_t columns, pvlc_hip_gemv_tiled_plan *o
 // Workspace layout of the paged decode.
 struct DecodeWorkspace {
     size_t part_o_offset, part_ml_offset, counters_offset, error_offset, total;
+    uint32_t part_stride;  // partials per (sequence, kv head) slot: max_parts rounded up to odd
 };
 DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts);
 // Partition rules: balanced_parts is the partition count per (sequence, kv

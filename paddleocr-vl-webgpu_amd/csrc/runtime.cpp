@@ -153,10 +153,17 @@ pvlc_hip_status launch_decode_checked(const pvlc_hip_paged_decode_args *a, void 
                         shape.pairs,
                         streaming,
                         max_parts,
+                        layout.part_stride,
                         reinterpret_cast<float *>(ws + layout.part_o_offset),
                         reinterpret_cast<float *>(ws + layout.part_ml_offset),
                         reinterpret_cast<uint32_t *>(ws + layout.counters_offset),
-                        reinterpret_cast<uint32_t *>(ws + layout.error_offset)};
+                        reinterpret_cast<uint32_t *>(ws + layout.error_offset),
+                        nullptr};
+    // The words after the error word (inside its 256-byte slot) carry the
+    // partition an automatic streaming launch settled on and the compute
+    // units it assumed.
+    if (streaming && a->partition_tokens == 0)
+        launch.partition_word = reinterpret_cast<uint32_t *>(ws + layout.error_offset) + 1;
     const int e = launch_paged_decode(launch, stream);
     if (e != 0) return hip_fail(static_cast<hipError_t>(e), "paged decode launch");
     return PVLC_HIP_OK;

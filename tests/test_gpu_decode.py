@@ -270,11 +270,13 @@ def test_no_rotary_small_contexts():
         check_device_layers(r, 2, prefix, rope=False, label=f"norope p={prefix}")
 
 
-def paged_case(num_seqs, lo, hi, seed, partition=0, log_uniform=False, workspace=None):
-    """Ragged batch over a shared paged cache with seeded permuted block tables."""
+def paged_case(num_seqs, lo, hi, seed, partition=0, log_uniform=False, workspace=None, lens=None):
+    """Ragged batch over a shared paged cache with seeded permuted block tables.  Returns the workspace."""
     import torch
     rng = np.random.default_rng(seed)
-    if log_uniform:
+    if lens is not None:
+        lens = np.asarray(lens, np.int64)
+    elif log_uniform:
         lens = np.exp(rng.uniform(np.log(lo), np.log(hi), num_seqs)).astype(np.int64)
     else:
         lens = rng.integers(lo, hi + 1, num_seqs)
@@ -328,12 +330,37 @@ def paged_case(num_seqs, lo, hi, seed, partition=0, log_uniform=False, workspace
         np.testing.assert_array_equal(gv, np.concatenate([rows[s][1], nv[s * W:(s + 1) * W]]))
         want = O.decode_gqa_f32(widen(q[s * 2048:(s + 1) * 2048]), widen(gk), widen(gv), n + 1, 16, 2, 128)
         check_close(widen(out[s * 2048:(s + 1) * 2048]), want, f"paged seq {s} T={n + 1}")
+    return ws
 
 
 @pytest.mark.parametrize("partition", [0, 64, 80, 512])
 def test_paged_ragged_batch(partition):
     log(f"case: paged ragged 12 seqs partition={partition}")
     paged_case(12, 1, 3000, seed=900 + partition, partition=partition)
+
+
+def test_automatic_partition_balances_the_compute_units():
+    """Ragged lengths whose 512-token partitions make two items more than two per compute unit (on 256 units):
+    with an automatic partition the kernel picks, among P0 + c*P0/4 (c = 0..4), the one with the least
+    ceil(items / units) * P, and the merge kernel uses the same partition.  The choice and the unit count are read
+    back from the workspace header; outputs match the oracle whatever the choice."""
+    lens = [8192] * 15 + [8300]  # 15 * 16 + 17 = 257 partitions of 512 -> 514 items
+    log("case: automatic streaming partition, 16 seqs (15 x 8192, 8300)")
+    ws = paged_case(16, 0, 0, seed=990, lens=lens)
+    words = ws[:16].cpu().numpy().view(np.uint32)
+    chosen, units = int(words[1]), int(words[2])
+    assert units > 0
+    best, expected = None, None
+    for c in range(5):
+        pc = 512 + c * 128
+        items = 2 * sum((t + pc - 1) // pc for t in lens)
+        cost = -(-items // units) * pc
+        if best is None or cost < best:
+            best, expected = cost, pc
+    log(f"{units} compute units: partition {chosen} (expected {expected})")
+    assert chosen == expected
+    if units == 256:
+        assert chosen == 640  # 514 items at 512 (3 per unit), 416 at 640 (2 per unit)
 
 
 def test_paged_long_context_split_k():
