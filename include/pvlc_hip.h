@@ -340,12 +340,16 @@ typedef struct pvlc_hip_paged_decode_args {
     uint32_t rope_rows;
     const int32_t *positions; /* [num_seqs] rotary position of the new token, or NULL = cache_len */
     uint32_t rotate_query;    /* also rotate the query at that position */
-    uint32_t partition_tokens; /* split-K partition (64..4096, multiple of 64); 0 = automatic */
+    uint32_t partition_tokens; /* split-K partition (16..4096, multiple of 16); 0 = automatic */
     void *workspace;           /* from pvlc_hip_paged_decode_workspace_bytes, initialised once */
     size_t workspace_bytes;
 } pvlc_hip_paged_decode_args;
 
-/* Partition size the automatic choice (partition_tokens = 0) uses. */
+/* Partition size the automatic choice (partition_tokens = 0) plans with.  A
+ * streaming launch (ragged cache_lens, or contexts beyond one round of
+ * single-shot workgroups) may lengthen it on the device, to at most twice this,
+ * so the items spread evenly over the compute units; it records the partition
+ * it used in the workspace word after the error word. */
 uint32_t pvlc_hip_paged_decode_partition(uint32_t num_seqs, uint32_t max_context);
 /* Workspace for split-K partials, merge counters and the device error word. */
 size_t pvlc_hip_paged_decode_workspace_bytes(uint32_t num_seqs, uint32_t max_context, uint32_t partition_tokens);
