@@ -247,6 +247,7 @@ def main() -> int:
                                "pct_hbm_peak": round(100 * sweep_gbps / HBM_PEAK_GBPS, 2),
                                "algorithmic_bytes": sweep_bytes,
                                "device_error_word": pvlc.workspace_error(ws, wsb, stream)}
+    result["inputs"] = {"generator": "numpy PCG64 standard_normal -> f32 -> fp16 (replica 0, the CPU baseline inputs), torch Philox randn on the device (replicas 1..)", "seeds": {"numpy": 2048, "torch": 7}, "note": "not the splitmix64/Box-Muller streams of the survey; timings do not depend on the N(0,1) generator"}
     print(json.dumps(result, ensure_ascii=False))
     return 0
 
@@ -361,6 +362,7 @@ def bench_batched(args):
         torch.cuda.synchronize()
         result["cpu_baseline"] = batched_cpu_baseline(pvlc, torch, planes[0], d_tables, num_blocks, lens, q, out,
                                                       args.cpu_seconds, step_bytes)
+    result["inputs"] = {"generator": "numpy PCG64 (lengths, block-table permutation), torch Philox randn on the device (caches, q, new K/V)", "seeds": {"numpy": args.config, "torch": args.config}}
     print(json.dumps(result, ensure_ascii=False))
     return 0
 
@@ -449,6 +451,7 @@ def bench_prefill(args):
                                                  "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4)}}
     if not args.no_cpu:
         result["cpu_baseline"] = prefill_cpu_baseline(pvlc, torch, n, nb, q, kp, vp, out, args.cpu_seconds, flops)
+    result["inputs"] = {"generator": "torch Philox randn on the device, x0.5", "seeds": {"torch": 4}}
     print(json.dumps(result, ensure_ascii=False))
     return 0
 
@@ -619,6 +622,7 @@ def bench_gemv(args):
     }
     if not args.no_cpu:
         result["cpu_baseline"] = gemv_cpu_baseline(separate, logits, args.cpu_seconds, step_bytes)
+    result["inputs"] = {"generator": "torch Philox randn on the device", "seeds": {"torch": 11}}
     print(json.dumps(result, ensure_ascii=False))
     return 0
 
@@ -733,6 +737,7 @@ def bench_projection(args):
         "dtype": "f16 weights, f32 activations split into fp16 hi+lo, f32 accumulate",
         "config": {"workload": "N=4096: q|k|v 2560x1024, o 1024x2048, gate|up 6144x1024, down 1024x3072, + bias"},
         "achieved_tflops": round(tflops, 1), "per_projection": per,
+        "inputs": {"generator": "torch Philox randn on the device", "seeds": {"torch": 12}},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(tflops / 2500.0, 4),
                      "note": "algorithmic FLOPs (2*N*out*in); the device issues two fp16 MFMAs per product, so "
