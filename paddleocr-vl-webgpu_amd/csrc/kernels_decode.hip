@@ -136,7 +136,7 @@ __device__ inline void load_chunk(const DecodeParams &p, uint32_t g, uint32_t id
 // reported after the key/value loads are consumed, so no conditional memory
 // operation sits among them.
 template <int WAVES, int PAIRS, bool DEFER_MERGE>
-__device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g, uint32_t part, int cache_len,
+__device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uint32_t g, uint32_t part, int cache_len,
                                    int pos, uint32_t ids, bool ids_bad) {
     constexpr int kChunkTiles = 2 * PAIRS;         // 16-token tiles a wave holds in registers at once
     constexpr int kChunkTokens = kChunkTiles * 16;
@@ -146,8 +146,7 @@ __device__ inline void decode_item(const DecodeParams &p, uint32_t s, uint32_t g
     const int kg = lane >> 4;   // MFMA k-group of this lane
     constexpr int kThreads = WAVES * 64;
 
-    const int T = cache_len + 1;  // rows attended after the append
-    const int P = static_cast<int>(p.partition_tokens);
+    const int T = cache_len + 1;  // rows attended after the append (P: the partition length)
     const int part_start = static_cast<int>(part) * P;
     if (part_start >= T) return;
     const int part_end = min(part_start + P, T);
@@ -552,7 +551,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     const uint32_t ids =
         wave_tile_ids<WAVES, 2 * PAIRS>(p, s, part_start, min(part_start + P, cache_len + 1), wave, &bad);
     const int pos = p.positions ? load_const(p.positions, s) : cache_len;
-    decode_item<WAVES, PAIRS, false>(p, s, g, part, cache_len, pos, ids, bad);
+    decode_item<WAVES, PAIRS, false>(p, static_cast<int>(p.partition_tokens), s, g, part, cache_len, pos, ids, bad);
 }
 
 // Exclusive scan of one int per thread over the workgroup; *total receives
@@ -684,8 +683,6 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
         *part_out = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(k - sm_first[lo]));
     };
     const int items = total * static_cast<int>(kKvHeads);
-    DecodeParams q = p;
-    q.partition_tokens = static_cast<uint32_t>(P);
     int item = blockIdx.x;
     if (item >= items) return;
     uint32_t s = 0, part = 0;
@@ -703,7 +700,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
                                                    min(static_cast<int>(part_next + 1) * P, sm_len[s_next] + 1), wave,
                                                    &bad_next);
         }
-        decode_item<WAVES, PAIRS, true>(q, s, static_cast<uint32_t>(item & 1), part, sm_len[s], sm_pos[s], ids, bad);
+        decode_item<WAVES, PAIRS, true>(p, P, s, static_cast<uint32_t>(item & 1), part, sm_len[s], sm_pos[s], ids, bad);
         if (next >= items) break;
         __syncthreads();  // the next item reuses the workgroup's LDS
         item = next;
