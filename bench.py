@@ -553,6 +553,20 @@ def bench_gemv(args):
         for w_, x_, o_, r_, c_ in calls:
             pvlc.gemv_f16(w_, x_, o_, r_, c_, st)
 
+    # The same 127 GEMVs with the projections that read one hidden state grouped into one launch each
+    # (pvlc_hip_gemv_group_f16: q|k|v, gate|up), weights left in their own tensors: 73 launches.
+    def step_grouped(calls, st=stream):
+        for layer in range(LAYERS):
+            q_, k_, v_, o_, gate_, up_, down_ = calls[7 * layer:7 * layer + 7]
+            for members in ((q_, k_, v_), (o_,), (gate_, up_), (down_,)):
+                if len(members) == 1:
+                    w_, x_, out_, r_, c_ = members[0]
+                    pvlc.gemv_f16(w_, x_, out_, r_, c_, st)
+                else:
+                    pvlc.gemv_group_f16([(m[0], m[2], m[3]) for m in members], members[0][1], members[0][4], st)
+        for w_, x_, o_, r_, c_ in calls[7 * LAYERS:]:
+            pvlc.gemv_f16(w_, x_, o_, r_, c_, st)
+
     torch.cuda.synchronize()
     if args.profile_steps:
         # the step, then the LM head fused with the top-1 and the standalone top-1 over its logits
@@ -562,11 +576,13 @@ def bench_gemv(args):
         result = torch.zeros(2, dtype=torch.int32, device=dev)
         for _ in range(args.profile_steps):
             step(separate)
+            step_grouped(separate)
             pvlc.lm_head_top1_f16(head_w, inputs[1024], logits, GEMV_HEAD[1], GEMV_HEAD[2], result, tws, nbytes,
                                   stream)
             pvlc.logits_top1_f32(logits, GEMV_HEAD[1], result, tws, nbytes, stream)
         torch.cuda.synchronize()
-        print(json.dumps({"profile_steps": args.profile_steps, "launches_per_step": len(separate) + 2}))
+        print(json.dumps({"profile_steps": args.profile_steps,
+                          "launches_per_step": len(separate) + 4 * LAYERS + 1 + 2}))
         return 0
     for _ in range(args.warmup):
         step(separate)
@@ -577,8 +593,11 @@ def bench_gemv(args):
     # The decode loop captures its launches once and replays them: the same kernels and arguments as the eager
     # launches, replayed from a HIP graph (the first replay is checked against the eager outputs bit for bit).
     graph_sep, graph_fused = _gemv_graph(torch, step, separate), _gemv_graph(torch, step, fused)
-    ms = _timed_launches(torch, stream, steps, lambda i: graph_sep.replay())
+    graph_grp = _gemv_graph(torch, step_grouped, separate)
+    ms_sep = _timed_launches(torch, stream, steps, lambda i: graph_sep.replay())
     ms_fused = _timed_launches(torch, stream, steps, lambda i: graph_fused.replay())
+    ms = _timed_launches(torch, stream, steps, lambda i: graph_grp.replay())
+    ms_grp_eager = _timed_launches(torch, stream, steps, lambda i: step_grouped(separate))
     gbps = step_bytes / (ms * 1e-3) / 1e9
     gbps_fused = fused_bytes / (ms_fused * 1e-3) / 1e9
 
@@ -608,8 +627,13 @@ def bench_gemv(args):
         "data": "synthetic N(0,1)*0.02 fp16 weights, N(0,1) f32 vectors, seeded",
         "config": {"workload": "one decoder token step's weight GEMVs: 18 x (q 2048x1024, k/v 256x1024, o 1024x2048, "
                                "gate/up 3072x1024, down 1024x3072) + LM head 103424x1024, each layer its own weights",
-                   "launches_per_step": len(separate), "launch": "HIP graph replay of the step's launches"},
-        "eager_us": round(ms_eager * 1e3, 2),
+                   "launches_per_step": 4 * LAYERS + 1,
+                   "launch": "HIP graph replay; q|k|v and gate|up of a layer as one grouped launch each "
+                             "(pvlc_hip_gemv_group_f16), weights in their own tensors"},
+        "eager_us": round(ms_grp_eager * 1e3, 2),
+        "separate_launches": {"launches_per_step": len(separate), "us": round(ms_sep * 1e3, 2),
+                              "eager_us": round(ms_eager * 1e3, 2),
+                              "gbps": round(step_bytes / (ms_sep * 1e-3) / 1e9, 1)},
         "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,

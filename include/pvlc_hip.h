@@ -445,6 +445,24 @@ pvlc_hip_status pvlc_hip_gemv_tiled_plan_create(uint32_t rows, uint32_t columns,
 pvlc_hip_status pvlc_hip_gemv_f16(const uint16_t *weights, const float *vector, float *out, uint32_t rows,
                                   uint32_t columns, void *stream);
 
+/* Up to 4 GEMVs of one width that read the same vector, in one launch: member
+ * i writes members[i].out[r] = sum_c members[i].weights[r][c] * vector[c] for
+ * r < members[i].rows, with pvlc_hip_gemv_f16's arithmetic (results
+ * bit-identical to separate calls); the members' total rows are admitted as
+ * one pvlc_hip_gemv_f16.  For the projections that read the same normalised
+ * hidden state (q, k and v of a layer; gate and up), which the reference
+ * dispatches as separate gemv_tiled_f16_weights passes (pvlc-wgsl
+ * lib.rs:1770-1835, decoder_stack_session.rs): one launch instead of three or
+ * two, weights left in their own tensors.  No single reference entry point
+ * corresponds to it. */
+typedef struct pvlc_hip_gemv_member {
+    const uint16_t *weights; /* [rows][columns] fp16, output-major */
+    float *out;              /* [rows] f32 */
+    uint32_t rows;
+} pvlc_hip_gemv_member;
+pvlc_hip_status pvlc_hip_gemv_group_f16(const pvlc_hip_gemv_member *members, uint32_t count, const float *vector,
+                                        uint32_t columns, void *stream);
+
 /* ---------------------------------------------------------------------------
  * LM head and greedy top-1 on the device.
  * ------------------------------------------------------------------------- */

@@ -210,6 +210,7 @@ SIGNATURES = {
     "pvlc_hip_kv_unpack_f16": ([_VP, _VP, _U32, _VP, _U32, _VP, _VP, _VP], ctypes.c_int32),
     "pvlc_hip_gemv_tiled_plan_create": ([_U32, _U32, ctypes.POINTER(GemvTiledPlanC)], ctypes.c_int32),
     "pvlc_hip_gemv_f16": ([_VP, _VP, _VP, _U32, _U32, _VP], ctypes.c_int32),
+    "pvlc_hip_gemv_group_f16": ([_VP, _U32, _VP, _U32, _VP], ctypes.c_int32),
     "pvlc_hip_top1_workspace_bytes": ([], _SZ),
     "pvlc_hip_paged_prefill_workspace_bytes": ([_U32], _SZ),
     "pvlc_hip_projection_plan_create": ([_U32, _U32, _U32, _U32, ctypes.POINTER(ProjectionPlanC)], ctypes.c_int32),
@@ -403,6 +404,20 @@ def gemv_f16(weights, vector, out, rows: int, columns: int, stream=None) -> None
     """out[r] = sum_c weights[r][c] * vector[c] (fp16 weights, f32 vector and output): replaces
     gemv_tiled_f16_weights (pvlc-wgsl lib.rs:1770-1835); admission as plan_gemv_tiled."""
     _check(lib.pvlc_hip_gemv_f16(_ptr(weights), _ptr(vector), _ptr(out), rows, columns, _stream(stream)))
+
+
+class GemvMemberC(ctypes.Structure):
+    _fields_ = [("weights", ctypes.c_void_p), ("out", ctypes.c_void_p), ("rows", ctypes.c_uint32)]
+
+
+def gemv_group_f16(members, vector, columns: int, stream=None) -> None:
+    """Up to 4 GEMVs (weights, out, rows) of one width reading the same vector, in one launch; each member's
+    output is bit-identical to gemv_f16 on it (the projections sharing a hidden state: q, k, v; gate, up)."""
+    arr = (GemvMemberC * max(1, len(members)))()
+    for i, (w, o, r) in enumerate(members):
+        arr[i] = GemvMemberC(_ptr(w), _ptr(o), r)
+    _check(lib.pvlc_hip_gemv_group_f16(ctypes.cast(arr, ctypes.c_void_p) if members else None, len(members),
+                                       _ptr(vector), columns, _stream(stream)))
 
 
 def top1_workspace_bytes() -> int:

@@ -152,6 +152,62 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_f16_kernel(const uint16_
     if constexpr (TOP1) top1_fold<kGemvWaves>(best, lds, slots);
 }
 
+// Global-memory access through an address picked as an integer: the cast to
+// the global address space keeps global_load (not flat_load, which also
+// drops the non-temporal hint).  Plain functions, not templates.
+typedef const __attribute__((address_space(1))) half8_t *global_half8_ptr;
+typedef __attribute__((address_space(1))) float *global_f32_ptr;
+__device__ inline half8_t load_half8_nt(uint64_t base, size_t element) {
+    return __builtin_nontemporal_load(reinterpret_cast<global_half8_ptr>(base + element * sizeof(uint16_t)));
+}
+__device__ inline void store_f32(uint64_t base, uint32_t index, float value) {
+    *reinterpret_cast<global_f32_ptr>(base + static_cast<uint64_t>(index) * sizeof(float)) = value;
+}
+
+// Grouped GEMV: up to kGemvGroupMax matrices of one width that read the same
+// vector (q, k and v of a layer; gate and up) in one launch, one row per wave
+// with the arithmetic of gemv_f16_kernel (results bit-identical to separate
+// launches).  Wave row i belongs to member m = the number of members that end
+// at or before it.  Every argument is used unconditionally (pointers picked
+// by masks, not branches), so they arrive in one batch of scalar loads rather
+// than a chain of dependent ones (a chain cost about 1 us per launch).
+template <int CHUNKS>
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_group_f16_kernel(GemvGroup g,
+                                                                           const float *__restrict__ vector) {
+    constexpr int kColumns = CHUNKS * 512;
+    const int lane = threadIdx.x & 63;
+    const uint32_t grow =
+        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * kGemvWaves + (threadIdx.x >> 6))));
+    const uint32_t rr = min(grow, g.total - 1);  // rows past the end re-read the last row, unstored
+    const uint32_t m = (rr >= g.end[0] ? 1u : 0u) + (rr >= g.end[1] ? 1u : 0u) + (rr >= g.end[2] ? 1u : 0u);
+    auto pick = [m](uint64_t a0, uint64_t a1, uint64_t a2, uint64_t a3) {
+        return (m == 0 ? a0 : 0ull) | (m == 1 ? a1 : 0ull) | (m == 2 ? a2 : 0ull) | (m == 3 ? a3 : 0ull);
+    };
+    const uint64_t wbase = pick(reinterpret_cast<uint64_t>(g.weights[0]), reinterpret_cast<uint64_t>(g.weights[1]),
+                                reinterpret_cast<uint64_t>(g.weights[2]), reinterpret_cast<uint64_t>(g.weights[3]));
+    const uint64_t obase = pick(reinterpret_cast<uint64_t>(g.out[0]), reinterpret_cast<uint64_t>(g.out[1]),
+                                reinterpret_cast<uint64_t>(g.out[2]), reinterpret_cast<uint64_t>(g.out[3]));
+    const uint32_t begin = static_cast<uint32_t>(pick(0, g.end[0], g.end[1], g.end[2]));
+    const uint32_t row = rr - begin;
+    half8_t w[CHUNKS];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) w[c] = load_half8_nt(wbase, static_cast<size_t>(row) * kColumns + (c * 64 + lane) * 8);
+    float4_t x[CHUNKS][2];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+        x[c][0] = *reinterpret_cast<const float4_t *>(vector + (c * 64 + lane) * 8);
+        x[c][1] = *reinterpret_cast<const float4_t *>(vector + (c * 64 + lane) * 8 + 4);
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(static_cast<float>(w[c][j]), x[c][j >> 2][j & 3], acc);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    if (grow < g.total && lane == 0) store_f32(obase, row, acc);
+}
+
 // Standalone top-1 over a logit row: a grid-stride scan in float4 lanes
 // (VEC: 16-byte aligned row) or scalars, then the same fold into the slots.
 template <bool VEC>
@@ -222,6 +278,18 @@ int launch_top1_finish(Top1Slot *slots, uint32_t *result, hipStream_t st) {
 }
 
 }  // namespace
+
+int launch_gemv_group_f16(const GemvGroup &group, const float *vector, uint32_t columns, void *stream) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const unsigned wgs = (group.total + kGemvWaves - 1) / kGemvWaves;
+    switch (columns) {
+        case 1024: hipLaunchKernelGGL(gemv_group_f16_kernel<2>, dim3(wgs), dim3(kGemvWaves * 64), 0, st, group, vector); break;
+        case 2048: hipLaunchKernelGGL(gemv_group_f16_kernel<4>, dim3(wgs), dim3(kGemvWaves * 64), 0, st, group, vector); break;
+        case 3072: hipLaunchKernelGGL(gemv_group_f16_kernel<6>, dim3(wgs), dim3(kGemvWaves * 64), 0, st, group, vector); break;
+        default: return static_cast<int>(hipErrorInvalidValue);
+    }
+    return static_cast<int>(hipGetLastError());
+}
 
 int launch_gemv_f16(const uint16_t *weights, const float *vector, float *out, uint32_t rows, uint32_t columns,
                     void *stream) {

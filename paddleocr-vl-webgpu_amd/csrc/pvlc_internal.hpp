@@ -184,6 +184,14 @@ inline PrefillWorkspace prefill_workspace_layout(uint32_t tokens) {
 }
 int launch_gemv_f16(const uint16_t *weights, const float *vector, float *out, uint32_t rows, uint32_t columns,
                     void *stream);
+constexpr uint32_t kGemvGroupMax = 4;
+struct GemvGroup {  // members of one grouped GEMV launch (by value: kernel argument)
+    const uint16_t *weights[kGemvGroupMax];
+    float *out[kGemvGroupMax];
+    uint32_t end[kGemvGroupMax - 1];  // rows up to the end of members 0..2; UINT32_MAX from the last member on
+    uint32_t total;                   // rows of all members
+};
+int launch_gemv_group_f16(const GemvGroup &group, const float *vector, uint32_t columns, void *stream);
 
 // Top-1 workspace: kTop1Slots slots of 256 bytes, each a packed u64
 // candidate; zero before the first launch, zero again after each launch.

@@ -493,6 +493,33 @@ pvlc_hip_status pvlc_hip_gemv_f16(const uint16_t *weights, const float *vector, 
     return ok();
 }
 
+pvlc_hip_status pvlc_hip_gemv_group_f16(const pvlc_hip_gemv_member *members, uint32_t count, const float *vector,
+                                        uint32_t columns, void *stream) {
+    if (!members || !vector) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "GEMV group members or vector pointer is NULL");
+    if (count == 0 || count > kGemvGroupMax)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "a GEMV group holds 1 to 4 members, not " + std::to_string(count));
+    GemvGroup g{};
+    for (uint32_t i = 0; i + 1 < kGemvGroupMax; ++i) g.end[i] = 0xFFFFFFFFu;
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (!members[i].weights || !members[i].out)
+            return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "GEMV group member " + std::to_string(i) + " has a NULL pointer");
+        if (members[i].rows == 0)
+            return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "GEMV group member " + std::to_string(i) + " has no rows");
+        total += members[i].rows;
+        if (total > 0xFFFFFFFFull) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "GEMV group rows overflow");
+        g.weights[i] = members[i].weights;
+        g.out[i] = members[i].out;
+        if (i + 1 < count) g.end[i] = static_cast<uint32_t>(total);
+    }
+    g.total = static_cast<uint32_t>(total);
+    // The launch is one GEMV of the members' total rows: admitted as such.
+    if (pvlc_hip_status st = plan_gemv_tiled(static_cast<uint32_t>(total), columns, nullptr)) return st;
+    const int e = launch_gemv_group_f16(g, vector, columns, stream);
+    if (e != 0) return hip_fail(static_cast<hipError_t>(e), "grouped GEMV launch");
+    return ok();
+}
+
 size_t pvlc_hip_top1_workspace_bytes(void) { return kTop1WorkspaceBytes; }
 
 namespace {

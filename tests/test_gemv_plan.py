@@ -130,3 +130,20 @@ def test_device_top1_entry_points_validate_before_touching_the_gpu():
     with pytest.raises(pvlc.PvlcHipError) as e:
         pvlc.lm_head_top1_f16(aligned, aligned, None, 103_424, 1024, aligned, None, nbytes)
     assert code(e.value) == ("InvalidInvocation", "LengthMismatch")
+
+
+def test_grouped_gemv_rejects_bad_groups_before_any_launch():
+    """pvlc_hip_gemv_group_f16 admission (no device work): 1..4 members, no NULL pointer, no empty member, total
+    rows and width admitted as one pvlc_hip_gemv_f16."""
+    with pytest.raises(pvlc.PvlcHipError):
+        pvlc.gemv_group_f16([], 1, 1024)
+    with pytest.raises(pvlc.PvlcHipError):
+        pvlc.gemv_group_f16([(1, 1, 8)] * 5, 1, 1024)
+    with pytest.raises(pvlc.PvlcHipError):
+        pvlc.gemv_group_f16([(1, 1, 8), (None, 1, 8)], 1, 1024)
+    with pytest.raises(pvlc.PvlcHipError):
+        pvlc.gemv_group_f16([(1, 1, 8), (1, 1, 0)], 1, 1024)
+    with pytest.raises(pvlc.PvlcHipError):
+        pvlc.gemv_group_f16([(1, 1, 8)], 1, 4096)
+    with pytest.raises(pvlc.PvlcHipError):
+        pvlc.gemv_group_f16([(1, 1, 8)], None, 1024)

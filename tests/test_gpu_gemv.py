@@ -77,3 +77,25 @@ def test_small_integers_are_exact_and_stream_argument_is_honoured():
     s.synchronize()
     np.testing.assert_array_equal(d_out.cpu().numpy(), wi @ xi)
     np.testing.assert_array_equal(O.linear_f32(xi, 1, columns, wi, np.zeros(rows, np.float32), rows), wi @ xi)
+
+
+@pytest.mark.parametrize("columns,rows", [(1024, (2048, 256, 256)), (1024, (3072, 3072)), (2048, (1024,)),
+                                          (3072, (1024, 5, 3, 1))])
+def test_grouped_gemv_equals_separate_calls(columns, rows):
+    """pvlc_hip_gemv_group_f16: every member's output equals pvlc_hip_gemv_f16 on that member bit for bit
+    (q, k, v of a layer; gate and up; ragged members); gemv_f16 itself is checked against the linear oracle
+    above, and no member writes past its rows."""
+    import torch
+    log(f"case: grouped GEMV columns={columns} rows={rows}")
+    g = torch.Generator(device="cuda").manual_seed(columns + sum(rows))
+    ws = [(torch.randn(r * columns, generator=g, device="cuda") * 0.05).half() for r in rows]
+    x = torch.randn(columns, generator=g, device="cuda")
+    sep = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+    grp = [torch.full((r + 4,), float("nan"), device="cuda") for r in rows]
+    for w, o, r in zip(ws, sep, rows):
+        pvlc.gemv_f16(w, x, o, r, columns)
+    pvlc.gemv_group_f16([(w, o, r) for w, o, r in zip(ws, grp, rows)], x, columns)
+    torch.cuda.synchronize()
+    for i, (a, b, r) in enumerate(zip(sep, grp, rows)):
+        assert torch.equal(a, b[:r]), f"member {i}"
+        assert torch.isnan(b[r:]).all(), f"member {i} wrote past its rows"
