@@ -62,6 +62,36 @@ def test_gemv_chain_and_lm_head_top1_replay_from_a_graph():
     assert int(ws.view(torch.int32).abs().sum().item()) == 0  # the slots come back cleared
 
 
+def test_grouped_gemv_stage_replays_from_a_graph():
+    """x -> (q, k, v) as one grouped launch -> o over q -> (gate, up) grouped over o's output: every replay,
+    with new inputs written eagerly in between, equals the same launches made eagerly."""
+    import torch
+    log("case: graph replay of grouped q|k|v -> o -> grouped gate|up")
+    wq, wk, wv = (to_dev(f16_bits(s, r * 1024, 0.03)) for s, r in ((11, 2048), (12, 256), (13, 256)))
+    wo = to_dev(f16_bits(14, 1024 * 2048, 0.03))
+    wg, wu = (to_dev(f16_bits(s, 3072 * 1024, 0.03)) for s in (15, 16))
+    x = torch.zeros(1024, dtype=torch.float32, device="cuda")
+    q, k, v = (torch.empty(r, dtype=torch.float32, device="cuda") for r in (2048, 256, 256))
+    o = torch.empty(1024, dtype=torch.float32, device="cuda")
+    gate, up = (torch.empty(3072, dtype=torch.float32, device="cuda") for _ in range(2))
+
+    def chain(stream):
+        pvlc.gemv_group_f16([(wq, q, 2048), (wk, k, 256), (wv, v, 256)], x, 1024, stream)
+        pvlc.gemv_f16(wo, q, o, 1024, 2048, stream)
+        pvlc.gemv_group_f16([(wg, gate, 3072), (wu, up, 3072)], o, 1024, stream)
+
+    graph = _capture(chain)
+    for rep in range(4):
+        x.copy_(to_dev_f32(np.random.default_rng(50 + rep).standard_normal(1024).astype(np.float32)))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in (q, k, v, o, gate, up)]
+        chain(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        for name, a, b in zip("q k v o gate up".split(), got, (q, k, v, o, gate, up)):
+            assert torch.equal(a, b), f"replay {rep}: {name}"
+
+
 def test_decode_step_replays_from_a_graph():
     import torch
     layers, prefix, capacity = 18, 2047, 2304
