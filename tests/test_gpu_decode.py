@@ -363,6 +363,14 @@ def test_automatic_partition_balances_the_compute_units():
         assert chosen == 640  # 514 items at 512 (3 per unit), 416 at 640 (2 per unit)
 
 
+def test_paged_maximum_merge_width():
+    """Config 5's longest contexts: 32768 rows at 512-token partitions is 64 partitions, the most one merge
+    combines (the plan rejects more); a neighbour at 32767 rows and a short one share the launch.  Cache rows
+    bit-exact, attention within tolerance of the oracle."""
+    log("case: paged decode at 64 partitions per merge (T = 32768, 32767, 1500; partition 512)")
+    paged_case(3, 0, 0, seed=970, partition=512, lens=[32768, 32767, 1500])
+
+
 def test_paged_long_context_split_k():
     log("case: paged long context (8 seqs, log-uniform [1024, 9000], partition 512)")
     paged_case(8, 1024, 9000, seed=950, partition=512, log_uniform=True)
