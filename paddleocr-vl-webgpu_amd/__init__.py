@@ -410,14 +410,26 @@ class GemvMemberC(ctypes.Structure):
     _fields_ = [("weights", ctypes.c_void_p), ("out", ctypes.c_void_p), ("rows", ctypes.c_uint32)]
 
 
+class GemvMembers:
+    """The members of a grouped GEMV as the C array pvlc_hip_gemv_group_f16 reads, built once (a decode loop
+    reuses its groups every token)."""
+
+    def __init__(self, members):
+        self.count = len(members)
+        self.array = (GemvMemberC * max(1, self.count))()
+        for i, (w, o, r) in enumerate(members):
+            self.array[i] = GemvMemberC(_ptr(w), _ptr(o), r)
+        self.keep = list(members)  # the tensors stay alive while the array points at them
+        self.pointer = ctypes.cast(self.array, ctypes.c_void_p) if self.count else None
+
+
 def gemv_group_f16(members, vector, columns: int, stream=None) -> None:
     """Up to 4 GEMVs (weights, out, rows) of one width reading the same vector, in one launch; each member's
-    output is bit-identical to gemv_f16 on it (the projections sharing a hidden state: q, k, v; gate, up)."""
-    arr = (GemvMemberC * max(1, len(members)))()
-    for i, (w, o, r) in enumerate(members):
-        arr[i] = GemvMemberC(_ptr(w), _ptr(o), r)
-    _check(lib.pvlc_hip_gemv_group_f16(ctypes.cast(arr, ctypes.c_void_p) if members else None, len(members),
-                                       _ptr(vector), columns, _stream(stream)))
+    output is bit-identical to gemv_f16 on it (the projections sharing a hidden state: q, k, v; gate, up).
+    `members` is a list of (weights, out, rows) or a prebuilt GemvMembers."""
+    if not isinstance(members, GemvMembers):
+        members = GemvMembers(members)
+    _check(lib.pvlc_hip_gemv_group_f16(members.pointer, members.count, _ptr(vector), columns, _stream(stream)))
 
 
 def top1_workspace_bytes() -> int:
