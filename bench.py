@@ -573,9 +573,6 @@ def bench_gemv(args):
             else:
                 pvlc.gemv_group_f16(group, x_, c_, st)
 
-        for w_, x_, o_, r_, c_ in calls[7 * LAYERS:]:
-            pvlc.gemv_f16(w_, x_, o_, r_, c_, st)
-
     torch.cuda.synchronize()
     if args.profile_steps:
         # the step, then the LM head fused with the top-1 and the standalone top-1 over its logits

@@ -347,10 +347,25 @@ typedef struct pvlc_hip_paged_decode_args {
 
 /* Partition size the automatic choice (partition_tokens = 0) plans with.  A
  * streaming launch (ragged cache_lens, or contexts beyond one round of
- * single-shot workgroups) may lengthen it on the device, to at most twice this,
- * so the items spread evenly over the compute units; it records the partition
- * it used in the workspace word after the error word. */
+ * single-shot workgroups) may lengthen it on the device, to at most twice this
+ * and at most 4096 tokens, so the items spread evenly over the compute units;
+ * it records the partition it used in the workspace word after the error word
+ * (pvlc_hip_paged_decode_streaming_partition gives the same choice on the
+ * host). */
 uint32_t pvlc_hip_paged_decode_partition(uint32_t num_seqs, uint32_t max_context);
+/* The partition an automatic launch over these ragged cache lengths (rows
+ * cached before the append; host memory, num_seqs entries) settles on, on a
+ * device of compute_units compute units: the planned partition P0 above, or
+ * the candidate P0 + c*max(16, P0/4 rounded down to 16), c = 1..4, with the
+ * least ceil(items / compute_units) * P, items counting (sequence, partition,
+ * kv head) triples -- never longer than the 4096 tokens one streaming
+ * workgroup covers.  The streaming kernel makes this choice on the device by
+ * the same rule and records it in the workspace word after the error word.
+ * Lengths outside 0..max_context-1 are not counted; 0 for NULL or empty
+ * input.  Host only.  (No reference counterpart: the reference plans fixed
+ * 32-key chunks, runtime-core lib.rs:2889-2978.) */
+uint32_t pvlc_hip_paged_decode_streaming_partition(const int32_t *cache_lens, uint32_t num_seqs, uint32_t max_context,
+                                                   uint32_t compute_units);
 /* Workspace for split-K partials, merge counters and the device error word. */
 size_t pvlc_hip_paged_decode_workspace_bytes(uint32_t num_seqs, uint32_t max_context, uint32_t partition_tokens);
 /* Zero a workspace on `stream` (a fill kernel; safe under graph capture). */

@@ -201,6 +201,7 @@ SIGNATURES = {
     "pvlc_hip_f32_to_f16_host": ([_F, _U16, _SZ], None),
     "pvlc_hip_f16_to_f32_host": ([_U16, _F, _SZ], None),
     "pvlc_hip_paged_decode_partition": ([_U32, _U32], _U32),
+    "pvlc_hip_paged_decode_streaming_partition": ([ctypes.POINTER(ctypes.c_int32), _U32, _U32, _U32], _U32),
     "pvlc_hip_paged_decode_workspace_bytes": ([_U32, _U32, _U32], _SZ),
     "pvlc_hip_workspace_init": ([_VP, _SZ, _VP], ctypes.c_int32),
     "pvlc_hip_workspace_error": ([_VP, _SZ, _VP, ctypes.POINTER(_U32)], ctypes.c_int32),
@@ -674,6 +675,13 @@ def _stream(stream) -> int | None:
 
 def decode_partition(num_seqs: int, max_context: int) -> int:
     return lib.pvlc_hip_paged_decode_partition(num_seqs, max_context)
+
+
+def decode_streaming_partition(cache_lens, max_context: int, compute_units: int) -> int:
+    """Partition an automatic launch over these ragged cache lengths settles on (host replay of the device rule)."""
+    lens = np.ascontiguousarray(np.asarray(cache_lens, dtype=np.int32).ravel())
+    return lib.pvlc_hip_paged_decode_streaming_partition(lens.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                                         len(lens), max_context, compute_units)
 
 
 def decode_workspace_bytes(num_seqs: int, max_context: int, partition_tokens: int = 0) -> int:

@@ -579,9 +579,6 @@ __device__ inline int workgroup_exclusive_scan(int v, int *sm_wave_sums, int *to
     return before + x - v;
 }
 
-// Partition lengths an automatic streaming launch chooses from: P0 + c P0/4.
-constexpr int kPartitionChoices = 5;
-
 // Persistent grid for ragged lengths and long contexts: every workgroup
 // reads the cache lengths (and positions) once into LDS, numbers the (sequence, partition,
 // kv head) items that hold rows, and walks items blockIdx.x,
@@ -601,7 +598,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
     const int i0 = static_cast<int>(threadIdx.x) * per;
     // Validity is judged against the partition the host planned with.
     const int P0 = static_cast<int>(p.partition_tokens);
-    const int step = max(16, (P0 / 4) & ~15);
+    static_assert(2 * PAIRS == 2, "wave_tile_ids holds 32 chunks of 2 tiles per wave");
+    constexpr uint32_t kSpan = streaming_span(WAVES);
     int counts[kPartitionChoices] = {};
     for (int i = i0; i < min(i0 + per, n); ++i) {
         const int64_t len =
@@ -612,17 +610,18 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
         if (p.partition_word) {
 #pragma unroll
             for (int c = 0; c < kPartitionChoices; ++c) {
-                const int pc = P0 + c * step;
-                counts[c] += len < 0 ? 0 : static_cast<int>((len + pc) / pc);
+                const int pc = static_cast<int>(streaming_partition_candidate(static_cast<uint32_t>(P0), c, kSpan));
+                counts[c] += (len < 0 || pc == 0) ? 0 : static_cast<int>((len + pc) / pc);
             }
         }
     }
-    // Automatic partition.  Item k runs on workgroup k mod grid, and the
-    // grid fills every compute unit before it doubles up, so item k lands on
-    // unit k mod units: a unit streams ceil(items / units) items one after the
-    // other at the per-unit HBM rate.  Take the first of P0, P0 + P0/4, ...,
-    // 2 P0 with the least ceil(items / units) * P (every workgroup computes
-    // the same counts from the same lengths).
+    // Automatic partition (choose_streaming_partition): item k runs on
+    // workgroup k mod grid, and the grid fills every compute unit before it
+    // doubles up, so item k lands on unit k mod units and a unit streams
+    // ceil(items / units) items one after the other at the per-unit HBM rate.
+    // Every workgroup computes the same counts from the same lengths.  The
+    // candidates stop at kSpan, the tokens covered by the block ids the
+    // workgroup's waves hold (wave_tile_ids).
     int P = P0;
     if (p.partition_word) {
         const int wave = threadIdx.x >> 6;
@@ -635,18 +634,12 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
         }
         __syncthreads();
         const uint32_t units = max(1u, p.compute_units);
-        uint64_t best = ~0ull;
+        uint32_t items[kPartitionChoices] = {};
         for (int c = 0; c < kPartitionChoices; ++c) {
-            uint32_t items_c = 0;  // at most 2048 sequences x 64 partitions x 2 heads
-            for (int w = 0; w < WAVES; ++w) items_c += static_cast<uint32_t>(sm_counts[c][w]);
-            items_c *= kKvHeads;
-            const int pc = P0 + c * step;
-            const uint64_t cost = static_cast<uint64_t>((items_c + units - 1) / units) * static_cast<uint32_t>(pc);
-            if (cost < best) {
-                best = cost;
-                P = pc;
-            }
+            for (int w = 0; w < WAVES; ++w) items[c] += static_cast<uint32_t>(sm_counts[c][w]);
+            items[c] *= kKvHeads;  // at most 2048 sequences x 64 partitions x 2 heads
         }
+        P = static_cast<int>(choose_streaming_partition(items, static_cast<uint32_t>(P0), units, kSpan));
         P = __builtin_amdgcn_readfirstlane(P);  // uniform: keep the item arithmetic scalar
         if (blockIdx.x == 0 && threadIdx.x == 0) {
             p.partition_word[0] = static_cast<uint32_t>(P);

@@ -40,6 +40,43 @@ constexpr uint32_t kMaxBalancedParts = 16;
 // with more ragged sequences use one workgroup per (partition, head, sequence).
 constexpr uint32_t kMaxRaggedSeqs = 2048;
 
+// Automatic streaming partition.  The host plans p0; the streaming kernel may
+// lengthen it to a candidate p0 + c*step (c < kPartitionChoices, step = p0/4
+// rounded down to 16 tokens, at least 16), never beyond the span one
+// workgroup of the streaming shape covers: a wave keeps the block ids of its
+// tiles one per lane (64 lanes = 32 chunks of 2 tiles), and a chunk round of
+// `waves` waves covers waves x 2 tiles, so a partition spans at most
+// 32 x waves x 2 x 16 = 1024 x waves tokens (4096 for the 4-wave shape).
+// Candidates beyond the span are skipped (0 below).
+constexpr int kPartitionChoices = 5;
+constexpr uint32_t streaming_span(uint32_t waves) { return 1024u * waves; }
+constexpr uint32_t streaming_partition_candidate(uint32_t p0, int c, uint32_t span) {
+    const uint32_t quarter = (p0 / 4) & ~15u;
+    const uint32_t pc = p0 + static_cast<uint32_t>(c) * (quarter > 16 ? quarter : 16);
+    return pc <= span ? pc : 0;
+}
+// The candidate with the least ceil(items / units) * P (the first on ties),
+// where items[c] counts the (sequence, partition, kv head) items at candidate
+// c: item k runs on compute unit k mod units, so a unit streams
+// ceil(items / units) partitions one after the other.  p0 itself is a
+// candidate whenever p0 <= span, which the host's shape choice guarantees.
+constexpr uint32_t choose_streaming_partition(const uint32_t (&items)[kPartitionChoices], uint32_t p0,
+                                              uint32_t units, uint32_t span) {
+    const uint32_t u = units > 0 ? units : 1;
+    uint32_t best_p = p0;
+    uint64_t best = ~0ull;
+    for (int c = 0; c < kPartitionChoices; ++c) {
+        const uint32_t pc = streaming_partition_candidate(p0, c, span);
+        if (pc == 0) continue;
+        const uint64_t cost = static_cast<uint64_t>((items[c] + u - 1) / u) * pc;
+        if (cost < best) {
+            best = cost;
+            best_p = pc;
+        }
+    }
+    return best_p;
+}
+
 // Status of a failed call: RuntimeErrorCode in bits 8..15, InvocationErrorCode
 // in bits 0..7; records the message for pvlc_hip_last_error_message().
 pvlc_hip_status fail(int runtime_code, int invocation_code, const std::string &message);

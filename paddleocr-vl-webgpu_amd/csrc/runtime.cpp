@@ -484,6 +484,26 @@ uint32_t pvlc_hip_paged_decode_partition(uint32_t num_seqs, uint32_t max_context
     return auto_partition(num_seqs, max_context);
 }
 
+uint32_t pvlc_hip_paged_decode_streaming_partition(const int32_t *cache_lens, uint32_t num_seqs, uint32_t max_context,
+                                                   uint32_t compute_units) {
+    if (!cache_lens || num_seqs == 0 || max_context == 0) return 0;
+    const uint32_t p0 = auto_partition(num_seqs, max_context);
+    // Launches with more ragged sequences than the persistent kernel numbers
+    // run one workgroup per (partition, head, sequence) at the planned partition.
+    if (num_seqs > kMaxRaggedSeqs) return p0;
+    const uint32_t span = streaming_span(decode_shape(p0, true).waves);
+    uint32_t items[kPartitionChoices] = {};
+    for (uint32_t i = 0; i < num_seqs; ++i) {
+        const int64_t len = cache_lens[i];
+        if (len < 0 || len + 1 > static_cast<int64_t>(max_context)) continue;  // not attended by the launch
+        for (int c = 0; c < kPartitionChoices; ++c) {
+            const uint32_t pc = streaming_partition_candidate(p0, c, span);
+            if (pc != 0) items[c] += static_cast<uint32_t>((len + pc) / pc) * kKvHeads;
+        }
+    }
+    return choose_streaming_partition(items, p0, compute_units, span);
+}
+
 pvlc_hip_status pvlc_hip_gemv_f16(const uint16_t *weights, const float *vector, float *out, uint32_t rows,
                                   uint32_t columns, void *stream) {
     if (!weights || !vector || !out) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "GEMV buffer pointer is NULL");
