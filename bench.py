@@ -281,25 +281,24 @@ def _timed_launches(torch, stream, k, fn):
     return start.elapsed_time(end) / k
 
 
-def bench_batched(args):
-    """Configs 3 and 5: one decode step (append + GQA) for a ragged batch of
-    sequences over one paged cache with seeded permuted block tables."""
-    import torch
-
-    from __graft_entry__ import load_package
-
-    pvlc = load_package()
-    dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream()
-    rng = np.random.default_rng(args.config)
-    if args.config == 3:
+def batched_workload(config: int) -> dict:
+    """Seeded lengths and block tables of configs 3 and 5 (BASELINE configs[2] and [4]): numpy PCG64 seeded with
+    the config number draws the lengths (T, rows attended after the append), then a permutation of the blocks;
+    sequence i owns the next ceil(T_i / 16) blocks of that permutation, in order.  Config 5 runs 512-token
+    partitions, config 3 the automatic partition (0)."""
+    rng = np.random.default_rng(config)
+    if config == 3:
         num_seqs = 64
         lens = rng.integers(256, 8192 + 1, num_seqs)
         label = "config 3: 64 seqs, T~U[256,8192], 16-token paged blocks, permuted block tables"
-    else:
+        partition = 0
+    elif config == 5:
         num_seqs = 256
         lens = np.exp(rng.uniform(np.log(1024), np.log(32768), num_seqs)).astype(np.int64)
         label = "config 5: 256 seqs, T~logU[1024,32768], 512-token partitions + LSE merge"
+        partition = 512
+    else:
+        raise ValueError(f"config {config} is not a batched decode config")
     max_context = int(lens.max())
     max_blocks = (max_context + 15) // 16
     need = (lens + 15) // 16
@@ -310,6 +309,24 @@ def bench_batched(args):
     for i in range(num_seqs):
         tables[i, :need[i]] = perm[off:off + need[i]]
         off += need[i]
+    return dict(num_seqs=num_seqs, lens=lens, tables=tables, num_blocks=num_blocks, label=label,
+                partition=partition)
+
+
+def bench_batched(args):
+    """Configs 3 and 5: one decode step (append + GQA) for a ragged batch of
+    sequences over one paged cache with seeded permuted block tables."""
+    import torch
+
+    from __graft_entry__ import load_package
+
+    pvlc = load_package()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    wl = batched_workload(args.config)
+    num_seqs, lens, tables, num_blocks, label = wl["num_seqs"], wl["lens"], wl["tables"], wl["num_blocks"], wl["label"]
+    max_context = int(lens.max())
+    max_blocks = tables.shape[1]
     gen = torch.Generator(device=dev).manual_seed(args.config)
     plane = num_blocks * 16 * W
     # Caches under ~600 MB are rotated over replicas so every step reads HBM,
@@ -328,7 +345,7 @@ def bench_batched(args):
     d_lens = torch.from_numpy((lens - 1).astype(np.int32)).to(dev)  # rows cached; the step appends one
     cos, sin = pvlc.rope_table(ROPE_BASE, max_context)
     d_cos, d_sin = torch.from_numpy(cos.ravel()).to(dev), torch.from_numpy(sin.ravel()).to(dev)
-    part = args.partition if args.partition else (512 if args.config == 5 else 0)
+    part = args.partition if args.partition else wl["partition"]
     wsb = pvlc.decode_workspace_bytes(num_seqs, max_context, part)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     pvlc.workspace_init(ws, wsb, stream)
