@@ -175,9 +175,17 @@ pvlc_hip_status pvlc_hip_prefill_plan_check(uint32_t tokens, uint32_t cache_capa
 typedef struct pvlc_hip_runtime pvlc_hip_runtime;
 typedef struct pvlc_hip_kv_session pvlc_hip_kv_session;
 
-/* NativeOptions, native lib.rs:268-271 (the observer is replaced by counters). */
+/* NativeOptions, native lib.rs:268-271 (the observer is replaced by counters).
+ * Every wait for submitted GPU work (session creation, step, finish, and the
+ * one-shot call) is bounded by gpu_wait_timeout_ns (0: 30 s, GPU_WAIT_TIMEOUT
+ * of native lib.rs:56).  A wait that expires fails with PVLC_HIP_OPERATION,
+ * and a session step that fails so leaves the session terminally poisoned
+ * (decoder_kv_session.rs:729-735, :513-528).  A session whose GPU work never
+ * completes keeps its device buffers allocated when it is destroyed, rather
+ * than freeing memory a kernel may still access. */
 typedef struct pvlc_hip_runtime_options {
-    int32_t device; /* HIP device ordinal */
+    int32_t device;               /* HIP device ordinal */
+    uint64_t gpu_wait_timeout_ns; /* 0 = 30 s */
 } pvlc_hip_runtime_options;
 
 /* Per-runtime counters (RuntimeCounters, native lib.rs:134-145). */
@@ -192,6 +200,11 @@ typedef struct pvlc_hip_runtime_counters {
 /* NativeRuntime::new, native lib.rs:912-1018.  Fails with
  * PVLC_HIP_ADAPTER_UNAVAILABLE when no gfx950 device is visible. */
 pvlc_hip_status pvlc_hip_runtime_create(const pvlc_hip_runtime_options *options, pvlc_hip_runtime **runtime_out);
+/* Sessions borrow their runtime, as NativeDecoderKvSession<'runtime> borrows
+ * NativeRuntime (decoder_kv_session.rs:23-30): destroying a runtime whose
+ * sessions are still live defers its release to the last of them (finish or
+ * destroy); those sessions keep working until then.  No other call may use
+ * the runtime after this one. */
 void pvlc_hip_runtime_destroy(pvlc_hip_runtime *runtime);
 pvlc_hip_status pvlc_hip_runtime_counters_get(const pvlc_hip_runtime *runtime, pvlc_hip_runtime_counters *out);
 
@@ -275,6 +288,14 @@ void pvlc_hip_kv_session_destroy(pvlc_hip_kv_session *session);
  * observer (decoder_kv_session_native_contract.rs:848-909): the next step
  * fails after its GPU work is submitted, which poisons the session. */
 void pvlc_hip_kv_session_fail_next_step_after_submit(pvlc_hip_kv_session *session);
+
+/* Fault injection for tests, standing in for a GPU that does not finish
+ * within the wait bound: the next bounded wait of this session (its next step
+ * or its finish) reports the deadline as passed whatever the GPU's state, so
+ * the call fails with PVLC_HIP_OPERATION and a step leaves the session
+ * poisoned, as the reference's poll timeout does (decoder_kv_session.rs:729-735).
+ * The submitted work itself runs to completion. */
+void pvlc_hip_kv_session_expire_next_wait(pvlc_hip_kv_session *session);
 
 /* ---------------------------------------------------------------------------
  * Device-resident hot path (fp16, caller stream, no allocation, no sync).

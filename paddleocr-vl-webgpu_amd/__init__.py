@@ -129,7 +129,7 @@ class KvStepPlanC(ctypes.Structure):
 
 
 class RuntimeOptionsC(ctypes.Structure):
-    _fields_ = [("device", ctypes.c_int32)]
+    _fields_ = [("device", ctypes.c_int32), ("gpu_wait_timeout_ns", ctypes.c_uint64)]
 
 
 class RuntimeCountersC(ctypes.Structure):
@@ -196,6 +196,7 @@ SIGNATURES = {
                                    ctypes.c_int32),
     "pvlc_hip_kv_session_destroy": ([_VP], None),
     "pvlc_hip_kv_session_fail_next_step_after_submit": ([_VP], None),
+    "pvlc_hip_kv_session_expire_next_wait": ([_VP], None),
     "pvlc_hip_rope_table_f32": ([ctypes.c_float, _U32, _U32, _F, _F], ctypes.c_int32),
     "pvlc_hip_mrope_table_f32": ([_F, _F, _U32, _U32, _U32, _U32, _F, _F], ctypes.c_int32),
     "pvlc_hip_f32_to_f16_host": ([_F, _U16, _SZ], None),
@@ -556,11 +557,15 @@ def f16_to_f32(bits) -> np.ndarray:
 # --------------------------------------------------------------------------
 
 class NativeRuntime:
-    """pvlc-runtime-native NativeRuntime (lib.rs:724-745, 912-1018) on one HIP device."""
+    """pvlc-runtime-native NativeRuntime (lib.rs:724-745, 912-1018) on one HIP device.
 
-    def __init__(self, device: int = 0):
+    Every wait for submitted GPU work is bounded by ``gpu_wait_timeout_ns`` (0: 30 s, GPU_WAIT_TIMEOUT of
+    lib.rs:56); an expired wait raises Operation and poisons the session that waited."""
+
+    def __init__(self, device: int = 0, gpu_wait_timeout_ns: int = 0):
         handle = _VP()
-        _check(lib.pvlc_hip_runtime_create(ctypes.byref(RuntimeOptionsC(device)), ctypes.byref(handle)))
+        _check(lib.pvlc_hip_runtime_create(ctypes.byref(RuntimeOptionsC(device, gpu_wait_timeout_ns)),
+                                           ctypes.byref(handle)))
         self._handle = handle
 
     def close(self) -> None:
@@ -646,6 +651,10 @@ class NativeDecoderKvSession:
 
     def fail_next_step_after_submit(self) -> None:
         lib.pvlc_hip_kv_session_fail_next_step_after_submit(self._live())
+
+    def expire_next_wait(self) -> None:
+        """Test hook: the next bounded GPU wait (step or finish) reports its deadline as passed."""
+        lib.pvlc_hip_kv_session_expire_next_wait(self._live())
 
     def __del__(self):
         if getattr(self, "_handle", None):

@@ -29,7 +29,6 @@
 
 #include <cstdint>
 #include <mutex>
-#include <vector>
 
 #include "pvlc_device.hpp"
 #include "pvlc_internal.hpp"
@@ -766,7 +765,9 @@ __global__ void fill_u32_kernel(uint32_t *dst, size_t words, uint32_t value) {
 }  // namespace
 
 // Workgroups of `kernel` the current device keeps resident at once (compute
-// units x workgroups per unit), at most max_items; cached per kernel and device.
+// units x workgroups per unit), at most max_items; cached per kernel and device
+// in a fixed table (no allocation after the first launches; a full table only
+// means the query is repeated).
 uint32_t resident_workgroups(const void *kernel, int threads, uint64_t max_items, uint32_t *units, int *err) {
     struct Entry {
         const void *kernel;
@@ -774,8 +775,10 @@ uint32_t resident_workgroups(const void *kernel, int threads, uint64_t max_items
         uint32_t wgs;
         uint32_t cus;
     };
+    constexpr int kEntries = 256;
     static std::mutex mu;
-    static std::vector<Entry> cache;
+    static Entry cache[kEntries];
+    static int cached = 0;
     int device = 0;
     if (hipError_t r = hipGetDevice(&device)) {
         *err = static_cast<int>(r);
@@ -784,10 +787,10 @@ uint32_t resident_workgroups(const void *kernel, int threads, uint64_t max_items
     uint32_t wgs = 0, cus_seen = 0;
     {
         std::lock_guard<std::mutex> lock(mu);
-        for (const Entry &c : cache)
-            if (c.kernel == kernel && c.device == device) {
-                wgs = c.wgs;
-                cus_seen = c.cus;
+        for (int i = 0; i < cached; ++i)
+            if (cache[i].kernel == kernel && cache[i].device == device) {
+                wgs = cache[i].wgs;
+                cus_seen = cache[i].cus;
             }
     }
     if (wgs == 0) {
@@ -803,7 +806,7 @@ uint32_t resident_workgroups(const void *kernel, int threads, uint64_t max_items
         wgs = static_cast<uint32_t>(cus * (per_cu > 0 ? per_cu : 1));
         cus_seen = static_cast<uint32_t>(cus > 0 ? cus : 1);
         std::lock_guard<std::mutex> lock(mu);
-        cache.push_back({kernel, device, wgs, cus_seen});
+        if (cached < kEntries) cache[cached++] = {kernel, device, wgs, cus_seen};
     }
     *units = cus_seen;
     return static_cast<uint32_t>(max_items < wgs ? (max_items ? max_items : 1) : wgs);

@@ -257,6 +257,27 @@ struct DecodeWorkspace {
     uint32_t part_stride;  // partials per (sequence, kv head) slot: max_parts rounded up to odd
 };
 DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts);
+// Split-K state of one decode launch: partial outputs and (max, sum), merge
+// counters (zero before the launch; every launch leaves them zero), the error
+// word and the two status words (automatic streaming partition, compute
+// units).
+struct DecodeState {
+    float *part_o;
+    float *part_ml;
+    uint32_t *counters;
+    uint32_t *error_word;
+    uint32_t *status_words;
+    uint32_t part_stride;  // partials per (sequence, kv head) slot: max_parts rounded up to odd
+};
+// Checks of pvlc_hip_paged_decode_f16's arguments, the workspace aside: the
+// partition and the partitions per (sequence, kv head) of the launch.
+pvlc_hip_status validate_decode_geometry(const pvlc_hip_paged_decode_args *a, uint32_t *partition_out,
+                                         uint32_t *max_parts_out);
+// Launch a validated decode with its split-K state at `state`; launches_out
+// receives the kernels launched (1, or 2 for the persistent kernel and its
+// merge kernel).
+pvlc_hip_status launch_decode_state(const pvlc_hip_paged_decode_args *a, uint32_t partition, uint32_t max_parts,
+                                    const DecodeState &state, void *stream, uint32_t *launches_out);
 // Partition rules: balanced_parts is the partition count per (sequence, kv
 // head) of the single-shot rule; single_shot_partition returns 0 when a
 // partition would exceed kSingleShotTiles; auto_partition falls back to

@@ -20,6 +20,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "pvlc_internal.hpp"
@@ -29,8 +30,16 @@ using namespace pvlc;
 struct pvlc_hip_runtime {
     int device = 0;
     hipStream_t stream = nullptr;
+    hipEvent_t done = nullptr;     // recorded behind submitted work, polled by bounded waits
+    uint64_t wait_timeout_ns = 0;  // bound of every wait for submitted work
     std::mutex execution_lock;
     pvlc_hip_runtime_counters counters{};
+    // Sessions borrow their runtime (NativeDecoderKvSession<'runtime> in the
+    // reference): a runtime destroyed while sessions live is released by the
+    // last of them.
+    std::mutex life_lock;
+    uint32_t live_sessions = 0;
+    bool destroy_requested = false;
 };
 
 struct pvlc_hip_kv_session {
@@ -39,6 +48,7 @@ struct pvlc_hip_kv_session {
     uint32_t cache_tokens = 0;
     bool poisoned = false;
     bool fail_next_after_submit = false;
+    bool expire_next_wait = false;
     uint32_t num_blocks = 0;
     uint16_t *key_cache = nullptr;    // blocked planes
     uint16_t *value_cache = nullptr;
@@ -71,9 +81,51 @@ uint64_t now_ns() {
             .count());
 }
 
+// GPU_WAIT_TIMEOUT (native lib.rs:56): every wait for submitted work is
+// bounded, 30 s unless the runtime options give another bound.
+constexpr uint64_t kDefaultWaitTimeoutNs = 30ull * 1000 * 1000 * 1000;
+
+// Wait for everything queued on the runtime's stream so far, at most the
+// runtime's timeout: an event recorded behind the work is polled, first
+// spinning, then sleeping 20 us between polls.  Returns hipSuccess, the HIP
+// error of the queue, or hipErrorNotReady when the deadline passed with the
+// work still pending.  `expire` reports the deadline as passed at the first
+// poll whatever the GPU's state (the tests' stand-in for a GPU that does not
+// finish, so that no GPU is made to hang).
+hipError_t wait_bounded(pvlc_hip_runtime *rt, bool expire) {
+    if (hipError_t e = hipEventRecord(rt->done, rt->stream)) return e;
+    const uint64_t deadline = now_ns() + rt->wait_timeout_ns;
+    for (uint32_t polls = 0;; ++polls) {
+        const hipError_t e = expire ? hipErrorNotReady : hipEventQuery(rt->done);
+        if (e != hipErrorNotReady) return e;
+        if (expire || now_ns() >= deadline) return hipErrorNotReady;
+        if (polls >= 64) std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
+}
+
+// wait_bounded as a status: a wait that expires is an Operation failure, as
+// the reference's poll timeout is (decoder_kv_session.rs:729-735, :890-896).
+pvlc_hip_status wait_or_fail(pvlc_hip_runtime *rt, bool expire, const char *what) {
+    const hipError_t e = wait_bounded(rt, expire);
+    if (e == hipErrorNotReady)
+        return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE,
+                    std::string(what) + ": GPU work did not complete within " +
+                        std::to_string(rt->wait_timeout_ns / 1000000) + " ms");
+    if (e != hipSuccess) return hip_fail(e, what);
+    rt->counters.synchronizations += 1;
+    return PVLC_HIP_OK;
+}
+
+// Frees the session's buffers once the GPU work queued on the runtime has
+// completed (a bounded wait).  A session whose work does not complete within
+// the bound keeps its device buffers allocated (leaked) rather than freeing
+// memory a kernel may still access.
 void free_session_buffers(pvlc_hip_kv_session *s) {
     if (!s) return;
-    if (s->runtime) (void)hipSetDevice(s->runtime->device);
+    if (s->runtime) {
+        (void)hipSetDevice(s->runtime->device);
+        if (wait_bounded(s->runtime, false) == hipErrorNotReady) return;  // pinned staging may still be written
+    }
     (void)hipFree(s->key_cache);
     (void)hipFree(s->value_cache);
     (void)hipFree(s->step_operands);
@@ -85,14 +137,48 @@ void free_session_buffers(pvlc_hip_kv_session *s) {
     s->host_staging = nullptr;
 }
 
-// Device-resident argument validation shared by the public entry point and the
-// session path.  Returns a status (0 = ok) without touching the GPU.
-pvlc_hip_status validate_decode_args(const pvlc_hip_paged_decode_args *a, uint32_t *partition_out,
-                                     uint32_t *max_parts_out, DecodeWorkspace *layout_out) {
+void destroy_runtime_now(pvlc_hip_runtime *rt) {
+    (void)hipSetDevice(rt->device);
+    if (rt->done) (void)hipEventDestroy(rt->done);
+    if (rt->stream) (void)hipStreamDestroy(rt->stream);
+    delete rt;
+}
+
+// Releases a session: its buffers (after a bounded wait for the runtime's
+// queued work), the session, and its hold on the runtime, which the last
+// session of a destroyed runtime releases.  `lock_held`: the caller holds the
+// runtime's execution lock.
+void release_session(pvlc_hip_kv_session *s, bool lock_held) {
+    if (!s) return;
+    pvlc_hip_runtime *rt = s->runtime;
+    {
+        std::unique_lock<std::mutex> guard(rt->execution_lock, std::defer_lock);
+        if (!lock_held) guard.lock();
+        free_session_buffers(s);
+    }
+    delete s;
+    bool last = false;
+    {
+        std::lock_guard<std::mutex> life(rt->life_lock);
+        last = --rt->live_sessions == 0 && rt->destroy_requested;
+    }
+    if (last) destroy_runtime_now(rt);
+}
+
+}  // namespace
+
+namespace pvlc {
+
+// Device-resident argument validation, the workspace aside, shared by the
+// public entry points and the session path: the partition and the
+// partitions per (sequence, kv head) the launch runs.  Returns a status
+// (0 = ok) without touching the GPU.
+pvlc_hip_status validate_decode_geometry(const pvlc_hip_paged_decode_args *a, uint32_t *partition_out,
+                                         uint32_t *max_parts_out) {
     if (!a) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "paged decode args are NULL");
     if (a->num_seqs == 0 || a->num_blocks == 0 || a->max_blocks_per_seq == 0 || a->max_context == 0)
         return invalid(PVLC_HIP_INV_ZERO_DIMENSION, "all paged decode dimensions must be nonzero");
-    if (!a->key_cache || !a->value_cache || !a->query || !a->new_key || !a->new_value || !a->out || !a->workspace)
+    if (!a->key_cache || !a->value_cache || !a->query || !a->new_key || !a->new_value || !a->out)
         return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "paged decode buffer pointer is NULL");
     if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr) || (a->rope_cos && a->rope_rows == 0))
         return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION, "rotary tables must be given together with rows");
@@ -127,21 +213,13 @@ pvlc_hip_status validate_decode_args(const pvlc_hip_paged_decode_args *a, uint32
     if (max_parts > kMaxMergeParts)
         return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY,
                        "the context needs more than the 64 partitions one merge combines");
-    const DecodeWorkspace layout = decode_workspace_layout(a->num_seqs, max_parts);
-    if (a->workspace_bytes < layout.total)
-        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "workspace holds " + std::to_string(a->workspace_bytes) +
-                                                         " bytes but the launch needs " + std::to_string(layout.total));
     if (partition_out) *partition_out = partition;
     if (max_parts_out) *max_parts_out = max_parts;
-    if (layout_out) *layout_out = layout;
     return PVLC_HIP_OK;
 }
 
-pvlc_hip_status launch_decode_checked(const pvlc_hip_paged_decode_args *a, void *stream) {
-    uint32_t partition = 0, max_parts = 0;
-    DecodeWorkspace layout{};
-    if (pvlc_hip_status st = validate_decode_args(a, &partition, &max_parts, &layout)) return st;
-    char *ws = static_cast<char *>(a->workspace);
+pvlc_hip_status launch_decode_state(const pvlc_hip_paged_decode_args *a, uint32_t partition, uint32_t max_parts,
+                                    const DecodeState &state, void *stream, uint32_t *launches_out) {
     // Streaming regime: ragged lengths, or partitions longer than one chunk
     // of the largest single-shot workgroup.
     const uint32_t part_tiles = (partition + kBlockTokens - 1) / kBlockTokens;
@@ -153,20 +231,44 @@ pvlc_hip_status launch_decode_checked(const pvlc_hip_paged_decode_args *a, void 
                         shape.pairs,
                         streaming,
                         max_parts,
-                        layout.part_stride,
-                        reinterpret_cast<float *>(ws + layout.part_o_offset),
-                        reinterpret_cast<float *>(ws + layout.part_ml_offset),
-                        reinterpret_cast<uint32_t *>(ws + layout.counters_offset),
-                        reinterpret_cast<uint32_t *>(ws + layout.error_offset),
+                        state.part_stride,
+                        state.part_o,
+                        state.part_ml,
+                        state.counters,
+                        state.error_word,
                         nullptr};
-    // The words after the error word (inside its 256-byte slot) carry the
-    // partition an automatic streaming launch settled on and the compute
-    // units it assumed.
-    if (streaming && a->partition_tokens == 0)
-        launch.partition_word = reinterpret_cast<uint32_t *>(ws + layout.error_offset) + 1;
+    // An automatic streaming launch records the partition it settled on and
+    // the compute units it assumed in the two status words.
+    if (streaming && a->partition_tokens == 0) launch.partition_word = state.status_words;
     const int e = launch_paged_decode(launch, stream);
     if (e != 0) return hip_fail(static_cast<hipError_t>(e), "paged decode launch");
+    if (launches_out) *launches_out = streaming ? 2u : 1u;  // persistent kernel + merge kernel, or one kernel
     return PVLC_HIP_OK;
+}
+
+}  // namespace pvlc
+
+namespace {
+
+// The caller's workspace checked and laid out (decode_workspace_layout): the
+// error word first, the two status words after it in the same 256-byte slot.
+pvlc_hip_status launch_decode_checked(const pvlc_hip_paged_decode_args *a, void *stream,
+                                      uint32_t *launches_out = nullptr) {
+    uint32_t partition = 0, max_parts = 0;
+    if (pvlc_hip_status st = validate_decode_geometry(a, &partition, &max_parts)) return st;
+    if (!a->workspace) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "paged decode workspace is NULL");
+    const DecodeWorkspace layout = decode_workspace_layout(a->num_seqs, max_parts);
+    if (a->workspace_bytes < layout.total)
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "workspace holds " + std::to_string(a->workspace_bytes) +
+                                                         " bytes but the launch needs " + std::to_string(layout.total));
+    char *ws = static_cast<char *>(a->workspace);
+    const DecodeState state{reinterpret_cast<float *>(ws + layout.part_o_offset),
+                            reinterpret_cast<float *>(ws + layout.part_ml_offset),
+                            reinterpret_cast<uint32_t *>(ws + layout.counters_offset),
+                            reinterpret_cast<uint32_t *>(ws + layout.error_offset),
+                            reinterpret_cast<uint32_t *>(ws + layout.error_offset) + 1,
+                            layout.part_stride};
+    return launch_decode_state(a, partition, max_parts, state, stream, launches_out);
 }
 
 // Session creation shared by begin_decoder_kv_session and the one-shot path.
@@ -176,6 +278,10 @@ pvlc_hip_status create_session(pvlc_hip_runtime *rt, const pvlc_hip_kv_session_p
     auto *s = new (std::nothrow) pvlc_hip_kv_session();
     if (!s) return fail(PVLC_HIP_OUT_OF_MEMORY, PVLC_HIP_INV_NONE, "session allocation failed");
     s->runtime = rt;
+    {
+        std::lock_guard<std::mutex> life(rt->life_lock);
+        rt->live_sessions += 1;
+    }
     s->plan = plan;
     s->cache_tokens = plan.initial_cache_tokens;
     s->num_blocks = (plan.cache_capacity + kBlockTokens - 1) / kBlockTokens;
@@ -185,8 +291,7 @@ pvlc_hip_status create_session(pvlc_hip_runtime *rt, const pvlc_hip_kv_session_p
     const size_t plane_elems = static_cast<size_t>(s->num_blocks) * kBlockTokens * kRowElems;
 
     auto cleanup = [&](pvlc_hip_status st) {
-        free_session_buffers(s);
-        delete s;
+        release_session(s, true);  // the caller holds the execution lock
         return st;
     };
     hipError_t e;
@@ -219,10 +324,9 @@ pvlc_hip_status create_session(pvlc_hip_runtime *rt, const pvlc_hip_kv_session_p
         return cleanup(hip_fail(e, "value cache upload"));
     const int fe = launch_fill_u32(static_cast<uint32_t *>(s->workspace), s->workspace_bytes / 4, 0u, st);
     if (fe != 0) return cleanup(hip_fail(static_cast<hipError_t>(fe), "workspace init"));
-    if ((e = hipStreamSynchronize(st)) != hipSuccess) return cleanup(hip_fail(e, "session creation"));
     rt->counters.host_to_device_copies += 2;
     rt->counters.kernel_launches += 1;
-    rt->counters.synchronizations += 1;
+    if (pvlc_hip_status ws = wait_or_fail(rt, false, "session creation")) return cleanup(ws);
     rt->counters.sessions_created += 1;
     *out = s;
     return PVLC_HIP_OK;
@@ -260,15 +364,17 @@ pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_oper
     a.partition_tokens = 0;
     a.workspace = s->workspace;
     a.workspace_bytes = s->workspace_bytes;
-    if (pvlc_hip_status st = launch_decode_checked(&a, rt->stream)) return st;
-    rt->counters.kernel_launches += 1;
+    uint32_t launches = 0;
+    if (pvlc_hip_status st = launch_decode_checked(&a, rt->stream, &launches)) return st;
+    rt->counters.kernel_launches += launches;
 
     uint16_t *result = stage + kStepElems;
     HIP_TRY(hipMemcpyAsync(result, s->attention, kQueryElems * 2, hipMemcpyDeviceToHost, rt->stream),
             "attention readback");
     rt->counters.device_to_host_copies += 1;
-    HIP_TRY(hipStreamSynchronize(rt->stream), "decoder KV session step");
-    rt->counters.synchronizations += 1;
+    const bool expire = s->expire_next_wait;
+    s->expire_next_wait = false;
+    if (pvlc_hip_status st = wait_or_fail(rt, expire, "decoder KV session step")) return st;
     if (s->fail_next_after_submit) {
         s->fail_next_after_submit = false;
         return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE, "decoder KV session step: injected failure after submission");
@@ -278,7 +384,7 @@ pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_oper
         exec->cache_tokens_before = s->cache_tokens;
         exec->cache_tokens_after = s->cache_tokens + 1;
         exec->queue_wall_time_ns = now_ns() - started;
-        exec->dispatch_count = 1;
+        exec->dispatch_count = launches;
     }
     return PVLC_HIP_OK;
 }
@@ -287,15 +393,31 @@ pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_oper
 pvlc_hip_status read_planes(pvlc_hip_kv_session *s, float *key_out, float *value_out) {
     pvlc_hip_runtime *rt = s->runtime;
     const size_t plane_elems = static_cast<size_t>(s->num_blocks) * kBlockTokens * kRowElems;
-    std::vector<uint16_t> kb(plane_elems), vb(plane_elems);
     HIP_TRY(hipSetDevice(rt->device), "hipSetDevice");
-    HIP_TRY(hipMemcpyAsync(kb.data(), s->key_cache, plane_elems * 2, hipMemcpyDeviceToHost, rt->stream),
+    // Pinned staging keeps both copies asynchronous, so the one wait below
+    // (bounded) covers them.
+    uint16_t *staged = nullptr;
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&staged), plane_elems * 4, hipHostMallocDefault),
+            "finish staging");
+    struct Release {
+        uint16_t *p;
+        bool keep = false;  // the copies may still write into it
+        ~Release() {
+            if (!keep) (void)hipHostFree(p);
+        }
+    } release{staged};
+    uint16_t *kb = staged, *vb = staged + plane_elems;
+    HIP_TRY(hipMemcpyAsync(kb, s->key_cache, plane_elems * 2, hipMemcpyDeviceToHost, rt->stream),
             "key cache readback");
-    HIP_TRY(hipMemcpyAsync(vb.data(), s->value_cache, plane_elems * 2, hipMemcpyDeviceToHost, rt->stream),
+    HIP_TRY(hipMemcpyAsync(vb, s->value_cache, plane_elems * 2, hipMemcpyDeviceToHost, rt->stream),
             "value cache readback");
-    HIP_TRY(hipStreamSynchronize(rt->stream), "decoder KV session finish");
     rt->counters.device_to_host_copies += 2;
-    rt->counters.synchronizations += 1;
+    const bool expire = s->expire_next_wait;
+    s->expire_next_wait = false;
+    if (pvlc_hip_status st = wait_or_fail(rt, expire, "decoder KV session finish")) {
+        release.keep = wait_bounded(rt, false) != hipSuccess;
+        return st;
+    }
     for (uint32_t t = 0; t < s->plan.cache_capacity; ++t) {
         for (uint32_t h = 0; h < kKvHeads; ++h) {
             for (uint32_t d = 0; d < kHeadDim; ++d) {
@@ -336,11 +458,15 @@ pvlc_hip_status pvlc_hip_runtime_create(const pvlc_hip_runtime_options *options,
     auto *rt = new (std::nothrow) pvlc_hip_runtime();
     if (!rt) return fail(PVLC_HIP_OUT_OF_MEMORY, PVLC_HIP_INV_NONE, "runtime allocation failed");
     rt->device = device;
+    rt->wait_timeout_ns = options && options->gpu_wait_timeout_ns ? options->gpu_wait_timeout_ns : kDefaultWaitTimeoutNs;
     hipError_t e = hipSetDevice(device);
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&rt->done, hipEventDisableTiming);
     if (e != hipSuccess) {
+        if (rt->stream) (void)hipStreamDestroy(rt->stream);
         delete rt;
-        return fail(PVLC_HIP_DEVICE_REQUEST, PVLC_HIP_INV_NONE, std::string("stream creation: ") + hipGetErrorString(e));
+        return fail(PVLC_HIP_DEVICE_REQUEST, PVLC_HIP_INV_NONE,
+                    std::string("stream and event creation: ") + hipGetErrorString(e));
     }
     *runtime_out = rt;
     return ok();
@@ -348,9 +474,13 @@ pvlc_hip_status pvlc_hip_runtime_create(const pvlc_hip_runtime_options *options,
 
 void pvlc_hip_runtime_destroy(pvlc_hip_runtime *runtime) {
     if (!runtime) return;
-    (void)hipSetDevice(runtime->device);
-    if (runtime->stream) (void)hipStreamDestroy(runtime->stream);
-    delete runtime;
+    bool now = false;
+    {
+        std::lock_guard<std::mutex> life(runtime->life_lock);
+        runtime->destroy_requested = true;
+        now = runtime->live_sessions == 0;
+    }
+    if (now) destroy_runtime_now(runtime);
 }
 
 pvlc_hip_status pvlc_hip_runtime_counters_get(const pvlc_hip_runtime *runtime, pvlc_hip_runtime_counters *out) {
@@ -392,6 +522,10 @@ void pvlc_hip_kv_session_fail_next_step_after_submit(pvlc_hip_kv_session *sessio
     if (session) session->fail_next_after_submit = true;
 }
 
+void pvlc_hip_kv_session_expire_next_wait(pvlc_hip_kv_session *session) {
+    if (session) session->expire_next_wait = true;
+}
+
 pvlc_hip_status pvlc_hip_kv_session_step(pvlc_hip_kv_session *session, const pvlc_hip_kv_step_operands *step,
                                          float *attention, size_t attention_len,
                                          pvlc_hip_kv_step_execution *execution_out) {
@@ -421,10 +555,7 @@ pvlc_hip_status pvlc_hip_kv_session_finish(pvlc_hip_kv_session *session, float *
     if (!session) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "session is NULL");
     struct Consume {
         pvlc_hip_kv_session *s;
-        ~Consume() {
-            free_session_buffers(s);
-            delete s;
-        }
+        ~Consume() { release_session(s, false); }  // after the execution lock below is released
     } consume{session};
     if (session->poisoned)
         return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE, "decoder KV session is terminally poisoned");
@@ -438,11 +569,7 @@ pvlc_hip_status pvlc_hip_kv_session_finish(pvlc_hip_kv_session *session, float *
     return ok();
 }
 
-void pvlc_hip_kv_session_destroy(pvlc_hip_kv_session *session) {
-    if (!session) return;
-    free_session_buffers(session);
-    delete session;
-}
+void pvlc_hip_kv_session_destroy(pvlc_hip_kv_session *session) { release_session(session, false); }
 
 pvlc_hip_status pvlc_hip_run_decoder_cached_gqa(pvlc_hip_runtime *runtime,
                                                 const pvlc_hip_cached_gqa_invocation *invocation,
@@ -471,8 +598,7 @@ pvlc_hip_status pvlc_hip_run_decoder_cached_gqa(pvlc_hip_runtime *runtime,
                                   invocation->appended_value_len};
     pvlc_hip_status st = execute_step(s, &step, execution->attention, nullptr);
     if (st == PVLC_HIP_OK) st = read_planes(s, execution->key_cache, execution->value_cache);
-    free_session_buffers(s);
-    delete s;
+    release_session(s, true);
     if (st != PVLC_HIP_OK) return st;
     execution->cache_tokens = sp.cache_tokens_after;
     execution->cache_capacity = plan.cache_capacity;

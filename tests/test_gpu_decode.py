@@ -138,6 +138,105 @@ def test_session_failure_after_submission_poisons(runtime):
     assert e.value.code == "Operation"
 
 
+def test_expired_gpu_wait_poisons_the_session(runtime):
+    """The reference bounds every wait by GPU_WAIT_TIMEOUT (native lib.rs:56) and fails the step with Operation
+    (decoder_kv_session.rs:729-735); the step had marked the session poisoned before submitting
+    (:513-528).  The hook reports the next wait's deadline as passed while the GPU work runs to completion, so
+    no GPU hangs.  A finish whose wait expires fails the same way; a fresh session on the runtime works."""
+    log("case: expired GPU wait poisons")
+    keys, values = session_inputs(75, 6, 12)
+    s = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(6, 12, keys, values))
+    s.step(pvlc.DecoderKvSessionStep(*step_inputs(76)))
+    s.expire_next_wait()
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        s.step(pvlc.DecoderKvSessionStep(*step_inputs(77)))
+    assert e.value.code == "Operation" and "did not complete within 30000 ms" in str(e.value)
+    assert s.poisoned and s.cache_tokens == 7
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        s.step(pvlc.DecoderKvSessionStep(*step_inputs(78)))
+    assert e.value.code == "Operation"
+    del s
+    t = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(6, 12, keys, values))
+    q, k, v = step_inputs(79)
+    out = t.step(pvlc.DecoderKvSessionStep(q, k, v)).attention
+    check_close(out, O.decode_gqa_f32(q, np.concatenate([keys[:6 * W], k]), np.concatenate([values[:6 * W], v]), 7,
+                                      16, 2, 128), "after an expired wait")
+    t.expire_next_wait()
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        t.finish()
+    assert e.value.code == "Operation"
+
+
+def test_wait_bound_is_a_runtime_option():
+    rt = pvlc.NativeRuntime(0, gpu_wait_timeout_ns=1_500_000_000)
+    keys, values = session_inputs(85, 3, 5)
+    s = rt.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(3, 5, keys, values))
+    s.expire_next_wait()
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        s.step(pvlc.DecoderKvSessionStep(*step_inputs(86)))
+    assert "within 1500 ms" in str(e.value)
+    del s
+    rt.close()
+
+
+def test_runtime_destroyed_before_its_sessions():
+    """Sessions borrow their runtime (NativeDecoderKvSession<'runtime>, decoder_kv_session.rs:23-30): a runtime
+    destroyed while sessions live is released by the last of them, and they keep working until then -- also a
+    session kept alive only by an exception's traceback, which is dropped after the runtime."""
+    rt = pvlc.NativeRuntime(0)
+    keys, values = session_inputs(87, 9, 20)
+    a = rt.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(9, 20, keys, values))
+    b = rt.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(9, 20, keys, values))
+    b.expire_next_wait()
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        b.step(pvlc.DecoderKvSessionStep(*step_inputs(88)))
+    del b
+    rt.close()
+    q, k, v = step_inputs(89)
+    out = a.step(pvlc.DecoderKvSessionStep(q, k, v)).attention
+    check_close(out, O.decode_gqa_f32(q, np.concatenate([keys[:9 * W], k]), np.concatenate([values[:9 * W], v]), 10,
+                                      16, 2, 128), "session after its runtime was destroyed")
+    snap = a.finish()
+    assert snap.cache_tokens == 10
+    del e  # drops the last reference to the poisoned session, after its runtime
+
+
+def counter_delta(before, after):
+    return {k: after[k] - before[k] for k in before}
+
+
+@pytest.mark.parametrize("prefix,capacity,launches", [(7, 13, 1), (7000, 7100, 2)])
+def test_session_effect_topology(prefix, capacity, launches):
+    """Exact per-call effects, as decoder_kv_session_native_contract.rs:411 asserts through its observer:
+    creation uploads both planes, clears the workspace with one fill kernel and waits once; a step uploads its
+    operands once, launches the decode (one kernel, or the persistent kernel and its merge kernel for contexts
+    beyond one round of single-shot workgroups), reads the attention back once and waits once; finish reads both
+    planes back and waits once; an invalid step has no effect at all."""
+    rt = pvlc.NativeRuntime(0)
+    keys, values = session_inputs(140, prefix, capacity)
+    c0 = rt.counters()
+    s = rt.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(prefix, capacity, keys, values))
+    c1 = rt.counters()
+    assert counter_delta(c0, c1) == {"kernel_launches": 1, "host_to_device_copies": 2, "device_to_host_copies": 0,
+                                     "synchronizations": 1, "sessions_created": 1}
+    q, k, v = step_inputs(141)
+    ex = s.step(pvlc.DecoderKvSessionStep(q, k, v))
+    c2 = rt.counters()
+    assert ex.dispatch_count == launches
+    assert counter_delta(c1, c2) == {"kernel_launches": launches, "host_to_device_copies": 1,
+                                     "device_to_host_copies": 1, "synchronizations": 1, "sessions_created": 0}
+    bad = q.copy()
+    bad[5] = np.inf
+    with pytest.raises(pvlc.PvlcHipError):
+        s.step(pvlc.DecoderKvSessionStep(bad, k, v))
+    assert rt.counters() == c2
+    s.finish()
+    c3 = rt.counters()
+    assert counter_delta(c2, c3) == {"kernel_launches": 0, "host_to_device_copies": 0, "device_to_host_copies": 2,
+                                     "synchronizations": 1, "sessions_created": 0}
+    rt.close()
+
+
 def test_interleaved_sessions_stay_independent(runtime):
     log("case: interleaved sessions")
     a_k, a_v = session_inputs(90, 33, 40)
@@ -249,11 +348,23 @@ def test_config1_rotary_append_at_1024():
     check_device_layers(r, 1, 1024, label="config1")
 
 
-@pytest.mark.parametrize("partition", [0, 48, 64, 128, 256, 304, 336, 512, 1024])
+@pytest.mark.parametrize("partition", [0, 48, 64, 128, 160, 192, 256, 304, 336, 512, 1024])
 def test_config2_18_layers_at_2048(partition):
     log(f"case: config 2 step (18 layers, T=2048, partition={partition})")
     r = device_decode(18, 2047, 2304, seed=600, partition=partition)
     check_device_layers(r, 18, 2047, label=f"config2 p={partition}")
+
+
+@pytest.mark.parametrize("prefix,planned", [(1280, 192), (1343, 192), (1344, 256), (1600, 256), (1791, 256),
+                                            (1792, 384), (2303, 384)])
+def test_config2_sweep_automatic_shapes(prefix, planned):
+    """The config-2 sweep (T = 1281..2304, 18 layers, capacity 2304) runs three automatic single-shot shapes:
+    192-token partitions (6 waves) up to T = 1344, 256 (8 waves) up to 1792, 384 (12 waves) beyond.  Both ends
+    of each range, against the oracle on every layer."""
+    assert pvlc.decode_partition(18, prefix + 1) == planned
+    log(f"case: config 2 sweep shape T={prefix + 1} (automatic partition {planned})")
+    r = device_decode(18, prefix, 2304, seed=3000 + prefix)
+    check_device_layers(r, 18, prefix, label=f"sweep T={prefix + 1}")
 
 
 def test_rotated_query_and_explicit_positions():
