@@ -407,6 +407,24 @@ pvlc_hip_status pvlc_hip_workspace_error(const void *workspace, size_t workspace
  * pvlc-runtime-web decoder_stack_session.rs:4698-4729) with one launch. */
 pvlc_hip_status pvlc_hip_paged_decode_f16(const pvlc_hip_paged_decode_args *args, void *stream);
 
+/* pvlc_hip_paged_decode_f16 without allocation: the same validation, kernels
+ * and results (bit-identical outputs and caches), with the split-K state kept
+ * in a file-scope device array of the library (16 MiB per device, held until
+ * the process ends) instead of a caller workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  args->workspace must be NULL and args->workspace_bytes 0.
+ * error_word (device, caller-zeroed) receives the device error bits of
+ * pvlc_hip_workspace_error.  At most 4096 sequences; a launch whose split-K
+ * state exceeds 16 MiB is rejected (InvalidDecoderGeometry) -- configs with
+ * up to 64 sequences of 8192 rows fit.  The first call on a device looks up
+ * the array's address there, clears its counters and waits for that clear on
+ * `stream` once; later calls never synchronise.  Every call on one device
+ * shares that device's array and leaves it ready for the next call: calls
+ * that overlap on one device (two streams, two threads) race. */
+pvlc_hip_status pvlc_hip_paged_decode_f16_no_alloc(const pvlc_hip_paged_decode_args *args, uint32_t *error_word,
+                                                   void *stream);
+
 typedef struct pvlc_hip_paged_prefill_args {
     uint32_t tokens;            /* N */
     uint32_t num_blocks;

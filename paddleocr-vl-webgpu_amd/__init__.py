@@ -207,6 +207,7 @@ SIGNATURES = {
     "pvlc_hip_workspace_init": ([_VP, _SZ, _VP], ctypes.c_int32),
     "pvlc_hip_workspace_error": ([_VP, _SZ, _VP, ctypes.POINTER(_U32)], ctypes.c_int32),
     "pvlc_hip_paged_decode_f16": ([ctypes.POINTER(PagedDecodeArgsC), _VP], ctypes.c_int32),
+    "pvlc_hip_paged_decode_f16_no_alloc": ([ctypes.POINTER(PagedDecodeArgsC), _VP, _VP], ctypes.c_int32),
     "pvlc_hip_paged_prefill_f16": ([ctypes.POINTER(PagedPrefillArgsC), _VP], ctypes.c_int32),
     "pvlc_hip_kv_pack_f16": ([_VP, _VP, _U32, _VP, _U32, _VP, _VP, _VP], ctypes.c_int32),
     "pvlc_hip_kv_unpack_f16": ([_VP, _VP, _U32, _VP, _U32, _VP, _VP, _VP], ctypes.c_int32),
@@ -721,6 +722,12 @@ def paged_decode_f16(args: PagedDecodeArgsC, stream=None) -> None:
     """One fused rotary+append+attention decode step for every sequence
     (replaces decoder_mrope/kv_append/gqa_split_partial/merge, wgsl lib.rs:927-1234)."""
     _check(lib.pvlc_hip_paged_decode_f16(ctypes.byref(args), _stream(stream)))
+
+
+def paged_decode_f16_no_alloc(args: PagedDecodeArgsC, error_word, stream=None) -> None:
+    """paged_decode_f16 with its split-K state in the library's per-device scratch (no workspace, no
+    allocation); the device error bits are OR-ed into ``error_word`` (a caller-zeroed device word)."""
+    _check(lib.pvlc_hip_paged_decode_f16_no_alloc(ctypes.byref(args), _ptr(error_word), _stream(stream)))
 
 
 def prefill_workspace_bytes(tokens: int) -> int:
