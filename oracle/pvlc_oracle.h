@@ -10,7 +10,7 @@
  * built with -O2 -ffp-contract=off and no fast-math, using glibc expf/powf/
  * sinf/cosf/sqrtf, so every rounding step matches the Rust original.
  *
- * Pinning (how each function is checked, see tests/test_oracle_*.py):
+ * Pinning (how each function is checked, see tests/test_oracle.py):
  *   oracle_decode_gqa_f32   reference digest DIRECT_BOUNDARY_BLAKE3, bounded
  *                           extreme [1.0, 3.0], physical-repeat equality,
  *                           wrong-grouping / missing-scale sensitivity, f64
