@@ -57,6 +57,12 @@ def parse():
     ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = automatic)")
     ap.add_argument("--replicas", type=int, default=12)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample")
+    ap.add_argument("--cpu-seconds-extra", type=float, default=5.0,
+                    help="bound of each CPU baseline sample of configs 3, 4 and 5 in the default run")
+    ap.add_argument("--only-config2", action="store_true",
+                    help="default run without the configs 3, 4 and 5 legs")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="HBM read probe: one launch streaming the config-2 step's bytes with several grids")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=0,
                     help="only run this many steps (no CPU leg), for rocprofv3 runs")
@@ -80,6 +86,8 @@ def main() -> int:
         return 2
     if args.calibrate_copy:
         return calibrate_copy(args)
+    if args.read_floor:
+        return bench_read_floor(args)
     if args.gemv:
         return bench_gemv(args)
     if args.projection:
@@ -94,6 +102,26 @@ def main() -> int:
     from __graft_entry__ import load_package
 
     pvlc = load_package()
+    result = measure_config2(pvlc, torch, args)
+    if result is None:  # --profile-steps
+        return 0
+    if not args.only_config2:
+        # The other configs of the benchmark plan, each with its own roofline and bounded CPU baseline.
+        extra = argparse.Namespace(**vars(args))
+        extra.cpu_seconds = args.cpu_seconds_extra
+        torch.cuda.empty_cache()
+        result["configs"] = {}
+        for c in (3, 5):
+            result["configs"][f"config{c}"] = measure_batched(pvlc, torch, c, extra)
+            torch.cuda.empty_cache()
+        result["configs"]["config4"] = measure_prefill(pvlc, torch, extra)
+        torch.cuda.empty_cache()
+    print(json.dumps(result, ensure_ascii=False))
+    return 0
+
+
+def measure_config2(pvlc, torch, args):
+    """Config 2's headline step (18 layers, T=2048, one fused launch) and its sweep; None with --profile-steps."""
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     nb_per = CAPACITY // 16
@@ -156,7 +184,7 @@ def main() -> int:
         run(args.profile_steps, len(replicas))
         torch.cuda.synchronize()
         print(json.dumps({"profile_steps": args.profile_steps, "partition": partition}))
-        return 0
+        return None
 
     def timed(k, rot):
         torch.cuda.synchronize()
@@ -175,6 +203,8 @@ def main() -> int:
     t0 = time.perf_counter()
     ms_per_step = timed(args.steps, len(replicas))
     wall = time.perf_counter() - t0
+    stats = _launch_stats(torch, stream, args.steps,
+                          lambda i: pvlc.paged_decode_f16(replicas[i % len(replicas)]["args"], stream))
     warm_ms = timed(args.steps, 1)
     err = pvlc.workspace_error(ws, wsb, stream)
 
@@ -213,6 +243,7 @@ def main() -> int:
                    "replica_bytes": replica_bytes},
         "achieved_gbps": round(gbps, 1),
         "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "launch_stats": stats,
         "warm_single_replica": {"us_per_step": round(warm_ms * 1e3, 3), "gbps": round(warm_gbps, 1),
                                 "note": "one replica re-read back to back: served largely from the Infinity "
                                         "Cache, not HBM"},
@@ -248,7 +279,60 @@ def main() -> int:
                                "algorithmic_bytes": sweep_bytes,
                                "device_error_word": pvlc.workspace_error(ws, wsb, stream)}
     result["inputs"] = {"generator": "numpy PCG64 standard_normal -> f32 -> fp16 (replica 0, the CPU baseline inputs), torch Philox randn on the device (replicas 1..)", "seeds": {"numpy": 2048, "torch": 7}, "note": "not the splitmix64/Box-Muller streams of the survey; timings do not depend on the N(0,1) generator"}
-    print(json.dumps(result, ensure_ascii=False))
+    del replicas, sweep
+    return result
+
+
+# Read-probe shapes (workgroups, waves, KiB per wave): the config-2 decode grid as launched (216 workgroups of 12
+# waves, 16 KiB each: the 37.75 MiB of keys and values plus the re-reads of short last partitions), then
+# 37.75 MiB exactly under other grids.
+READ_FLOOR_SHAPES = ((216, 12, 16), (288, 8, 16), (144, 16, 16), (576, 4, 16), (1152, 4, 8), (144, 8, 32),
+                     (256, 12, 8), (512, 12, 8))
+
+
+def bench_read_floor(args):
+    """One launch of a pure HBM read (paddleocr-vl-webgpu_amd/probes/hbm_read.hip) per shape: the time a launch
+    needs to stream the config-2 step's bytes with no compute and no merge, on cache-cold data (the windows rotate
+    through 600 MiB, beyond the 256 MiB Infinity Cache).  Mean of back-to-back launches and per-launch
+    percentiles, as for the decode step."""
+    import ctypes
+
+    import torch
+
+    from __graft_entry__ import load_package
+
+    load_package()  # torch first, then the HIP libraries: one HIP runtime in the process
+    probe = ctypes.CDLL(os.path.join(REPO, "paddleocr-vl-webgpu_amd", "libpvlc_probes.so"))
+    probe.pvlc_probe_hbm_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                          ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+    probe.pvlc_probe_hbm_read.restype = ctypes.c_int
+    stream = torch.cuda.current_stream()
+    pool = torch.randint(0, 2**31 - 1, ((600 << 20) // 4,), dtype=torch.int32, device="cuda")
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    rows = []
+    for wgs, waves, kib in READ_FLOOR_SHAPES:
+        nbytes = wgs * waves * kib * 1024
+        windows = pool.numel() * 4 // nbytes
+
+        def launch(i, wgs=wgs, waves=waves, kib=kib, nbytes=nbytes, windows=windows):
+            src = pool.data_ptr() + (i % windows) * nbytes
+            e = probe.pvlc_probe_hbm_read(src, sink.data_ptr(), wgs, waves, kib, 0x9E3779B9, stream.cuda_stream)
+            assert e == 0, f"probe launch failed: {e}"
+
+        for i in range(args.warmup):
+            launch(i)
+        ms = _timed_launches(torch, stream, args.steps, launch)
+        stats = _launch_stats(torch, stream, args.steps, launch)
+        rows.append({"workgroups": wgs, "waves": waves, "kib_per_wave": kib, "bytes": nbytes,
+                     "us": round(ms * 1e3, 3), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
+                     "launch_stats": stats})
+    step_bytes = LAYERS * algorithmic_bytes(CONTEXT)
+    best = min(rows, key=lambda r: r["us"] * step_bytes / r["bytes"])
+    print(json.dumps({"metric": "HBM read floor for the config-2 step's bytes (one launch, no compute)",
+                      "shapes": rows, "config2_step_bytes": step_bytes,
+                      "best_scaled_to_step_us": round(best["us"] * step_bytes / best["bytes"], 3),
+                      "steps": args.steps, "warmup": args.warmup}, ensure_ascii=False))
     return 0
 
 
@@ -279,6 +363,28 @@ def _timed_launches(torch, stream, k, fn):
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / k
+
+
+def _launch_stats(torch, stream, k, fn, group=10):
+    """Spread of the per-launch time over k back-to-back calls of fn(i) on `stream`: the calls run as k // group
+    groups of `group` launches, each group between one event pair (queued behind a GPU-side delay), and each
+    group gives one per-launch time (median, p10, p90 over the groups).  An event between every two launches
+    would add its own marker (~2.7 µs measured on a 12.7 µs decode step), so single launches are not timed
+    apart."""
+    groups = max(1, k // group)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2_000_000 + 60_000 * groups * group))
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
+    ev[0].record(stream)
+    for gi in range(groups):
+        for j in range(group):
+            fn(gi * group + j)
+        ev[gi + 1].record(stream)
+    torch.cuda.synchronize()
+    d = np.array([ev[i].elapsed_time(ev[i + 1]) * 1e3 / group for i in range(groups)])
+    return {"method": f"{groups} groups of {group} back-to-back launches, one event pair per group",
+            "median_us": round(float(np.median(d)), 3), "p10_us": round(float(np.percentile(d, 10)), 3),
+            "p90_us": round(float(np.percentile(d, 90)), 3), "mean_us": round(float(d.mean()), 3)}
 
 
 def batched_workload(config: int) -> dict:
@@ -314,20 +420,24 @@ def batched_workload(config: int) -> dict:
 
 
 def bench_batched(args):
-    """Configs 3 and 5: one decode step (append + GQA) for a ragged batch of
-    sequences over one paged cache with seeded permuted block tables."""
     import torch
 
     from __graft_entry__ import load_package
 
-    pvlc = load_package()
+    print(json.dumps(measure_batched(load_package(), torch, args.config, args), ensure_ascii=False))
+    return 0
+
+
+def measure_batched(pvlc, torch, config, args):
+    """Configs 3 and 5: one decode step (append + GQA) for a ragged batch of
+    sequences over one paged cache with seeded permuted block tables."""
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
-    wl = batched_workload(args.config)
+    wl = batched_workload(config)
     num_seqs, lens, tables, num_blocks, label = wl["num_seqs"], wl["lens"], wl["tables"], wl["num_blocks"], wl["label"]
     max_context = int(lens.max())
     max_blocks = tables.shape[1]
-    gen = torch.Generator(device=dev).manual_seed(args.config)
+    gen = torch.Generator(device=dev).manual_seed(config)
     plane = num_blocks * 16 * W
     # Caches under ~600 MB are rotated over replicas so every step reads HBM,
     # not the 256 MB Infinity Cache left warm by the previous step.
@@ -358,6 +468,7 @@ def bench_batched(args):
     for i in range(args.warmup):
         pvlc.paged_decode_f16(launches[i % reps], stream)
     ms = _timed_launches(torch, stream, args.steps, lambda i: pvlc.paged_decode_f16(launches[i % reps], stream))
+    stats = _launch_stats(torch, stream, args.steps, lambda i: pvlc.paged_decode_f16(launches[i % reps], stream))
     total_t = int(lens.sum())
     step_bytes = 1024 * total_t + num_seqs * 10240
     gbps = step_bytes / (ms * 1e-3) / 1e9
@@ -366,6 +477,7 @@ def bench_batched(args):
         "partition_tokens": part or pvlc.decode_partition(num_seqs, max_context)},
         "value": round(ms * 1e3, 2), "unit": "µs/step", "steps": args.steps, "warmup": args.warmup,
         "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "launch_stats": stats,
         "algorithmic_bytes": step_bytes, "device_error_word": pvlc.workspace_error(ws, wsb, stream),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
@@ -379,9 +491,9 @@ def bench_batched(args):
         torch.cuda.synchronize()
         result["cpu_baseline"] = batched_cpu_baseline(pvlc, torch, planes[0], d_tables, num_blocks, lens, q, out,
                                                       args.cpu_seconds, step_bytes)
-    result["inputs"] = {"generator": "numpy PCG64 (lengths, block-table permutation), torch Philox randn on the device (caches, q, new K/V)", "seeds": {"numpy": args.config, "torch": args.config}}
-    print(json.dumps(result, ensure_ascii=False))
-    return 0
+    result["inputs"] = {"generator": "numpy PCG64 (lengths, block-table permutation), torch Philox randn on the device (caches, q, new K/V)", "seeds": {"numpy": config, "torch": config}}
+    del planes, launches
+    return result
 
 
 def batched_cpu_baseline(pvlc, torch, plane, d_tables, num_blocks, lens, q, out, seconds, step_bytes, sample=6):
@@ -424,13 +536,17 @@ def batched_cpu_baseline(pvlc, torch, plane, d_tables, num_blocks, lens, q, out,
 
 
 def bench_prefill(args):
-    """Config 4: causal prefill of 4096 tokens (rotary on Q and K, rows written to
-    the paged cache) -- MFMA-bound."""
     import torch
 
     from __graft_entry__ import load_package
 
-    pvlc = load_package()
+    print(json.dumps(measure_prefill(load_package(), torch, args), ensure_ascii=False))
+    return 0
+
+
+def measure_prefill(pvlc, torch, args):
+    """Config 4: causal prefill of 4096 tokens (rotary on Q and K, rows written to
+    the paged cache) -- MFMA-bound."""
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     n = 4096
@@ -457,6 +573,7 @@ def bench_prefill(args):
     for i in range(args.warmup):
         call(i)
     ms = _timed_launches(torch, stream, args.steps, call)
+    stats = _launch_stats(torch, stream, args.steps, call)
     flops = 16 * (n * (n + 1) // 2) * 512
     tflops = flops / (ms * 1e-3) / 1e12
     result = {"metric": "causal prefill µs + MFMA TFLOP/s (% fp16 dense peak)", "config": {
@@ -464,13 +581,13 @@ def bench_prefill(args):
         "workspace_bytes": wsb},
         "value": round(ms * 1e3, 2), "unit": "µs/call", "steps": args.steps, "warmup": args.warmup,
         "achieved_tflops": round(tflops, 1), "pct_mfma_peak": round(100 * tflops / 2500.0, 2),
+        "launch_stats": stats, "launches_per_call": 2,
         "algorithmic_flops": flops, "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": 2500.0,
                                                  "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4)}}
     if not args.no_cpu:
         result["cpu_baseline"] = prefill_cpu_baseline(pvlc, torch, n, nb, q, kp, vp, out, args.cpu_seconds, flops)
     result["inputs"] = {"generator": "torch Philox randn on the device, x0.5", "seeds": {"torch": 4}}
-    print(json.dumps(result, ensure_ascii=False))
-    return 0
+    return result
 
 
 def prefill_cpu_baseline(pvlc, torch, n, nb, q, kp, vp, out, seconds, flops, sample=16):
