@@ -214,20 +214,24 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     for (int kb = 0; kb < 4; ++kb)
         if (row >= static_cast<int>(kGroup)) qb[kb] = half8_t{};
 
-    // Append: the workgroup whose partition holds the appended row rotates
-    // the new key, writes the new K/V row into the cache, and keeps it in LDS
-    // to stand in for that row of the tile loads (which may see the old row).
-    // Rotate-half in f32 exactly as apply_rope_neox (cpu-ref lib.rs:459-463):
-    // x'[d] = x[d]*cos + (-x[d+64])*sin and x'[d+64] = x[d+64]*cos + x[d]*sin,
-    // products rounded separately (no contraction in this file), then RNE to
-    // fp16.
+    // Append: the wave whose chunks hold the appended row's tile rotates the
+    // new key, writes the new K/V row into the cache, and keeps it in LDS to
+    // stand in for that row of its own tile loads (which may see the old
+    // row).  Only that wave reads the row back, so no barrier is needed: a
+    // workgroup barrier here held every wave of the appending workgroup until
+    // the slowest wave's first loads had returned (config 2: 12.66 -> 12.25
+    // us).  Rotate-half in f32 exactly as apply_rope_neox (cpu-ref
+    // lib.rs:459-463): x'[d] = x[d]*cos + (-x[d+64])*sin and
+    // x'[d+64] = x[d+64]*cos + x[d]*sin, products rounded separately (no
+    // contraction in this file), then RNE to fp16.
     const int append_tile = cache_len >> 4;
     const int append_row = cache_len & 15;
     const bool owns_append = (append_tile << 4) >= part_start && (append_tile << 4) < part_end;
     __shared__ uint16_t sm_new_k[kHeadDim];
     __shared__ uint16_t sm_new_v[kHeadDim];
     if (owns_append) {
-        if (wave == 0) {
+        const int rel = append_tile - (part_start >> 4);  // tile of the partition holding the row
+        if (wave == (rel / kChunkTiles) % WAVES) {
             uint16_t k_lo = nk_lo, k_hi = nk_hi;
             if (rope) {
                 const float x = static_cast<float>(__builtin_bit_cast(_Float16, nk_lo));
@@ -256,7 +260,6 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
                 p.value_cache[slab + (lane + 64) * 16 + append_row] = nv_hi;
             }
         }
-        __syncthreads();  // uniform: owns_append depends on the workgroup only
     }
 
     float m_run = -INFINITY;  // running max (log2 units) of head `row`
@@ -871,6 +874,7 @@ int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
         case 2: PVLC_DECODE_LAUNCH(2, 1); break;
         case 4: PVLC_DECODE_LAUNCH(4, 1); break;
         case 6: PVLC_DECODE_LAUNCH(6, 1); break;
+        case 10: PVLC_DECODE_LAUNCH(10, 1); break;
         case 12: PVLC_DECODE_LAUNCH(12, 1); break;
         default: PVLC_DECODE_LAUNCH(8, 1); break;
     }

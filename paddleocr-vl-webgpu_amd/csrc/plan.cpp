@@ -392,6 +392,7 @@ DecodeShape decode_shape(uint32_t partition_tokens, bool streaming) {
     if (tiles <= 8) return {4, 1};
     if (tiles <= 12) return {6, 1};
     if (tiles <= 16) return {8, 1};
+    if (tiles <= 20) return {10, 1};
     if (tiles <= 24) return {12, 1};
     return {8, 1};
 }
@@ -412,7 +413,7 @@ uint32_t single_shot_partition(uint32_t num_seqs, uint32_t context) {
     const uint32_t tiles = (context + kBlockTokens - 1) / kBlockTokens;
     const uint32_t parts = balanced_parts(num_seqs);
     uint32_t part_tiles = (tiles + parts - 1) / parts;
-    static const uint32_t kCapacities[] = {4, 8, 12, 16, 24};  // tiles of the single-shot shapes
+    static const uint32_t kCapacities[] = {4, 8, 12, 16, 20, 24};  // tiles of the single-shot shapes
     for (uint32_t c : kCapacities) {
         if (part_tiles <= c) return c * kBlockTokens;
     }

@@ -348,7 +348,7 @@ def test_config1_rotary_append_at_1024():
     check_device_layers(r, 1, 1024, label="config1")
 
 
-@pytest.mark.parametrize("partition", [0, 48, 64, 128, 160, 192, 256, 304, 336, 512, 1024])
+@pytest.mark.parametrize("partition", [0, 48, 64, 128, 160, 192, 256, 304, 320, 336, 384, 512, 1024])
 def test_config2_18_layers_at_2048(partition):
     log(f"case: config 2 step (18 layers, T=2048, partition={partition})")
     r = device_decode(18, 2047, 2304, seed=600, partition=partition)
@@ -356,11 +356,12 @@ def test_config2_18_layers_at_2048(partition):
 
 
 @pytest.mark.parametrize("prefix,planned", [(1280, 192), (1343, 192), (1344, 256), (1600, 256), (1791, 256),
-                                            (1792, 384), (2303, 384)])
+                                            (1792, 320), (2047, 320), (2239, 320), (2240, 384), (2303, 384)])
 def test_config2_sweep_automatic_shapes(prefix, planned):
-    """The config-2 sweep (T = 1281..2304, 18 layers, capacity 2304) runs three automatic single-shot shapes:
-    192-token partitions (6 waves) up to T = 1344, 256 (8 waves) up to 1792, 384 (12 waves) beyond.  Both ends
-    of each range, against the oracle on every layer."""
+    """The config-2 sweep (T = 1281..2304, 18 layers, capacity 2304) runs four automatic single-shot shapes:
+    192-token partitions (6 waves) up to T = 1344, 256 (8 waves) up to 1792, 320 (10 waves) up to 2240 (the
+    headline T = 2048 among them), 384 (12 waves) beyond.  Both ends of each range, against the oracle on every
+    layer."""
     assert pvlc.decode_partition(18, prefix + 1) == planned
     log(f"case: config 2 sweep shape T={prefix + 1} (automatic partition {planned})")
     r = device_decode(18, prefix, 2304, seed=3000 + prefix)

@@ -200,9 +200,10 @@ def test_rope_table_matches_reference_angle_formula():
 def test_decode_workspace_and_partition_rules():
     # balanced single-shot partitions: about 256 workgroups (one per compute unit) in one round,
     # at most 16 partitions per (sequence, kv head), whole 16-token tiles
-    # rounded up to whole waves (1, 2, 4 or a multiple of 8 tiles)
+    # rounded up to the tile capacity of a single-shot shape (4, 8, 12, 16, 20 or 24 tiles)
     assert pvlc.decode_partition(1, 1025) == 128         # 2 units: 5 tiles -> 8, 9 partitions
-    assert pvlc.decode_partition(18, 2048) == 384        # 36 units: 19 tiles -> 24, 6 partitions
+    assert pvlc.decode_partition(18, 2048) == 320        # 36 units: 19 tiles -> 20, 7 partitions (252 workgroups)
+    assert pvlc.decode_partition(18, 2304) == 384        # 36 units: 21 tiles -> 24, 6 partitions
     assert pvlc.decode_partition(64, 512) == 256         # 128 units x 2 partitions of 16 tiles
     assert pvlc.decode_partition(128, 96) == 128         # 256 units: one partition of 6 tiles -> 8
     # streaming partitions once one workgroup would need more than 32 tiles
