@@ -174,7 +174,7 @@ def measure_config2(pvlc, torch, args):
         replicas.append(dict(args=a, keep=(kp, vp, q, nk, nv, out)))
     torch.cuda.synchronize()
     replica_bytes = 2 * plane * 2
-    partition = args.partition or pvlc.decode_partition(LAYERS, CAPACITY)
+    partition = args.partition or pvlc.decode_partition(LAYERS, CONTEXT)  # the launch plans for its T rows
 
     def run(n, rot):
         for i in range(n):
