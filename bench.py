@@ -116,6 +116,8 @@ def main() -> int:
             torch.cuda.empty_cache()
         result["configs"]["config4"] = measure_prefill(pvlc, torch, extra)
         torch.cuda.empty_cache()
+        result["decoder_token_step"] = bench_token_chain(pvlc, torch, args)
+        torch.cuda.empty_cache()
     print(json.dumps(result, ensure_ascii=False))
     return 0
 
@@ -789,6 +791,159 @@ def bench_gemv(args):
     result["inputs"] = {"generator": "torch Philox randn on the device", "seeds": {"torch": 11}}
     print(json.dumps(result, ensure_ascii=False))
     return 0
+
+
+class TokenChain:
+    """One decoder token step as the reference's stack session issues it (web decoder_stack_session.rs:4625-4797),
+    on this backend's entry points, for `layers` layers at `context` rows attended after the append:
+
+        per layer: q|k|v  = grouped GEMV (pvlc_hip_gemv_group_f16) of the hidden state x   (f32 out)
+                   q|k|v -> fp16                                                            (torch copy)
+                   attn   = pvlc_hip_paged_decode_f16 over the layer's cache, num_seqs = 1: rotary on q and
+                            the new key, append at row context-1, GQA over `context` rows  (fp16 out)
+                   attn  -> f32                                                             (torch copy)
+                   o      = GEMV o (1024 x 2048)
+                   g|u    = grouped GEMV gate|up (3072 x 1024 each) of o
+                   x'     = GEMV down (1024 x 3072) of g
+        then the LM head fused with the greedy top-1 (pvlc_hip_lm_head_top1_f16) on the last x.
+
+    The decoder's norms, residual adds and SwiGLU are outside this backend and left out (down reads the gate
+    output directly); the data dependencies between layers are the decoder's.  Weights are seeded N(0,1)*0.02
+    fp16, caches N(0,1) fp16, each layer its own; per-layer q|k|v and attention outputs stay in their own
+    buffers so a test can check every layer."""
+
+    def __init__(self, pvlc, torch, layers, context, capacity, head_rows, seed=21):
+        dev = torch.device("cuda:0")
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        self.pvlc, self.torch, self.layers, self.context, self.head_rows = pvlc, torch, layers, context, head_rows
+        self.nb = (capacity + 15) // 16
+        plane = layers * self.nb * 16 * W
+
+        def weights(rows, columns):
+            return (torch.randn(rows * columns, generator=gen, device=dev) * 0.02).half()
+
+        self.kp = torch.randn(plane, generator=gen, device=dev, dtype=torch.float32).half()
+        self.vp = torch.randn(plane, generator=gen, device=dev, dtype=torch.float32).half()
+        self.w = [dict(q=weights(2048, 1024), k=weights(256, 1024), v=weights(256, 1024), o=weights(1024, 2048),
+                       gate=weights(3072, 1024), up=weights(3072, 1024), down=weights(1024, 3072))
+                  for _ in range(layers)]
+        self.head = weights(head_rows, 1024)
+        self.xs = [torch.randn(1024, generator=gen, device=dev)] + [torch.empty(1024, device=dev)
+                                                                    for _ in range(layers)]
+        self.qkv32 = [torch.empty(2560, device=dev) for _ in range(layers)]
+        self.qkv16 = [torch.empty(2560, dtype=torch.float16, device=dev) for _ in range(layers)]
+        self.attn16 = [torch.empty(2048, dtype=torch.float16, device=dev) for _ in range(layers)]
+        self.attn32 = torch.empty(2048, device=dev)
+        self.o32 = torch.empty(1024, device=dev)
+        self.gu32 = torch.empty(6144, device=dev)
+        self.logits = torch.empty(head_rows, device=dev)
+        self.result = torch.zeros(2, dtype=torch.int32, device=dev)
+        self.tws_bytes = pvlc.top1_workspace_bytes()
+        self.tws = torch.empty(self.tws_bytes, dtype=torch.uint8, device=dev)
+        pvlc.workspace_init(self.tws, self.tws_bytes)
+        cos, sin = pvlc.rope_table(ROPE_BASE, capacity)
+        self.cos, self.sin = torch.from_numpy(cos.ravel()).to(dev), torch.from_numpy(sin.ravel()).to(dev)
+        self.wsb = pvlc.decode_workspace_bytes(1, capacity)
+        self.ws = torch.empty(self.wsb, dtype=torch.uint8, device=dev)
+        pvlc.workspace_init(self.ws, self.wsb)
+        self.qkv_members, self.gu_members, self.decode_args = [], [], []
+        for l in range(layers):
+            q32 = self.qkv32[l]
+            self.qkv_members.append(pvlc.GemvMembers([(self.w[l]["q"], q32[:2048], 2048),
+                                                      (self.w[l]["k"], q32[2048:2304], 256),
+                                                      (self.w[l]["v"], q32[2304:], 256)]))
+            self.gu_members.append(pvlc.GemvMembers([(self.w[l]["gate"], self.gu32[:3072], 3072),
+                                                     (self.w[l]["up"], self.gu32[3072:], 3072)]))
+            off = l * self.nb * 16 * W
+            q16 = self.qkv16[l]
+            self.decode_args.append(pvlc.paged_decode_args(
+                num_seqs=1, num_blocks=self.nb, max_blocks_per_seq=self.nb, key_cache=self.kp[off:],
+                value_cache=self.vp[off:], query=q16[:2048], new_key=q16[2048:2304], new_value=q16[2304:],
+                out=self.attn16[l], workspace=self.ws, workspace_bytes=self.wsb, max_context=capacity,
+                uniform_cache_len=context - 1, rope_cos=self.cos, rope_sin=self.sin, rope_rows=capacity,
+                rotate_query=True))
+        torch.cuda.synchronize()
+
+    def layer(self, l, st):
+        pvlc = self.pvlc
+        pvlc.gemv_group_f16(self.qkv_members[l], self.xs[l], 1024, st)
+        self.qkv16[l].copy_(self.qkv32[l])
+        pvlc.paged_decode_f16(self.decode_args[l], st)
+        self.attn32.copy_(self.attn16[l])
+        pvlc.gemv_f16(self.w[l]["o"], self.attn32, self.o32, 1024, 2048, st)
+        pvlc.gemv_group_f16(self.gu_members[l], self.o32, 1024, st)
+        pvlc.gemv_f16(self.w[l]["down"], self.gu32[:3072], self.xs[l + 1], 1024, 3072, st)
+
+    def step(self, st):
+        """The whole token step on stream st (the current torch stream: the torch copies run there too)."""
+        for l in range(self.layers):
+            self.layer(l, st)
+        self.pvlc.lm_head_top1_f16(self.head, self.xs[self.layers], self.logits, self.head_rows, 1024, self.result,
+                                   self.tws, self.tws_bytes, st)
+
+    def attention_only(self, st):
+        """The 18 single-layer decode launches alone (the step's attention part)."""
+        for l in range(self.layers):
+            self.pvlc.paged_decode_f16(self.decode_args[l], st)
+
+    def capture(self, fn):
+        """Capture fn(stream) into a HIP graph on a side stream after one warm-up run there."""
+        torch = self.torch
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn(side)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        return graph
+
+    def state(self):
+        """Every buffer the step writes (for bit-exact comparisons)."""
+        return ([t.clone() for t in self.xs[1:]] + [t.clone() for t in self.qkv16] + [t.clone() for t in self.attn16]
+                + [self.logits.clone(), self.result.clone()])
+
+
+def bench_token_chain(pvlc, torch, args):
+    """The 18-layer decoder token step at T=2048 (TokenChain) replayed from a HIP graph, its attention launches
+    alone, and the same step launched eagerly; the first replay is checked against the eager step bit for bit."""
+    stream = torch.cuda.current_stream()
+    chain = TokenChain(pvlc, torch, LAYERS, CONTEXT, CAPACITY, GEMV_HEAD[1])
+    chain.step(stream)
+    torch.cuda.synchronize()
+    eager = chain.state()
+    graph = chain.capture(chain.step)
+    graph.replay()
+    torch.cuda.synchronize()
+    if not all(torch.equal(a, b) for a, b in zip(eager, chain.state())):
+        raise RuntimeError("token step replayed from a HIP graph differs from the eager launches")
+    att_graph = chain.capture(chain.attention_only)
+    steps = min(args.steps, 100)
+    for _ in range(3):
+        graph.replay()
+    ms_step = _timed_launches(torch, stream, steps, lambda i: graph.replay())
+    stats = _launch_stats(torch, stream, steps, lambda i: graph.replay())
+    ms_att = _timed_launches(torch, stream, steps, lambda i: att_graph.replay())
+    ms_eager = _timed_launches(torch, stream, min(steps, 20), lambda i: chain.step(stream))
+    weight_bytes = sum(gemv_bytes(r, c) for _, r, c in GEMV_LAYER) * LAYERS + gemv_bytes(GEMV_HEAD[1], GEMV_HEAD[2])
+    att_bytes = LAYERS * algorithmic_bytes(CONTEXT)
+    return {"workload": "one decoder token step at T=2048: 18 layers x (grouped q|k|v GEMV, fp16 conversion, "
+                        "single-layer paged decode with rotary q/k, append and GQA, f32 conversion, o GEMV, grouped "
+                        "gate|up GEMV, down GEMV) + LM head 103424x1024 fused with greedy top-1; norms and SwiGLU "
+                        "left out (outside this backend)",
+            "launches_per_step": LAYERS * 7 + 2,
+            "graph_us_per_token": round(ms_step * 1e3, 2), "graph_spread": stats,
+            "eager_us_per_token": round(ms_eager * 1e3, 2),
+            "attention_per_layer_us": round(ms_att * 1e3 / LAYERS, 3),
+            "attention_18_layers_us": round(ms_att * 1e3, 2),
+            "attention_note": "18 single-layer decode launches (1 MB of keys and values each) replayed from a "
+                              "graph back to back; config 2's headline runs the same 18 layers as one launch",
+            "bytes_per_token": weight_bytes + att_bytes,
+            "gbps": round((weight_bytes + att_bytes) / (ms_step * 1e-3) / 1e9, 1),
+            "replay_bit_exact_vs_eager": True}
 
 
 def _gemv_graph(torch, step, calls):
