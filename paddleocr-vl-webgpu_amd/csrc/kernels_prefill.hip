@@ -289,28 +289,30 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     // pick the global chunk that belongs at that LDS position of the layouts
     // above.  Steps past the end re-read the last tile (never used).
     typedef __attribute__((address_space(3))) void *lds_ptr;
-    auto dma_k = [&](int step, uint16_t *dst) {
-        // LDS chunk q = 64 k + lane (k = 4 wave + r): slot8 = lane & 7,
-        // tile = lane bit 3, h = lane bit 4, dim-chunk = 2 (k & 7) + lane bit 5, pair j = k >> 3
+    // ln: the lane id (passed in, so the last steps can use a separately
+    // computed copy; see the tail loop below).
+    auto dma_k = [&](int step, uint16_t *dst, int ln) {
+        // LDS chunk q = 64 k + ln (k = 4 wave + r): slot8 = ln & 7,
+        // tile = ln bit 3, h = ln bit 4, dim-chunk = 2 (k & 7) + ln bit 5, pair j = k >> 3
         const int j = wave >> 1;
         bool ok;
         const uint32_t b0 = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + 2 * j, last_tile)), &ok);
         const uint32_t b1 = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + 2 * j + 1, last_tile)), &ok);
-        const uint32_t blk = (lane & 8) ? b1 : b0;
+        const uint32_t blk = (ln & 8) ? b1 : b0;
         const uint16_t *src = p.key_cache + (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems +
-                              (((lane >> 4) & 1) * 8 + (lane & 7)) * 8 + (lane >> 5) * 128;
+                              (((ln >> 4) & 1) * 8 + (ln & 7)) * 8 + (ln >> 5) * 128;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int k = 4 * wave + r;
             __builtin_amdgcn_global_load_lds(src + (2 * (k & 7)) * 128, (lds_ptr)(dst + 64 * k * 8), 16, 0, 0);
         }
     };
-    auto dma_v = [&](int step, uint16_t *dst) {
-        // LDS chunk q = 64 k + lane: dim = (k & 1) 64 + lane, half = (k >> 1) & 1,
+    auto dma_v = [&](int step, uint16_t *dst, int ln) {
+        // LDS chunk q = 64 k + ln: dim = (k & 1) 64 + ln, half = (k >> 1) & 1,
         // tile = (k >> 2) & 1 = wave & 1, pair j = k >> 3 = wave >> 1
         bool ok;
         const uint32_t blk = cache_block(p, static_cast<uint32_t>(min(step * kStepTiles + wave, last_tile)), &ok);
-        const uint16_t *src = p.value_cache + (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems + lane * 16;
+        const uint16_t *src = p.value_cache + (static_cast<size_t>(blk) * kKvHeads + g) * kBlockHeadElems + ln * 16;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int k = 4 * wave + r;
@@ -424,9 +426,9 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     // K(i+1) from sk[(i+1)&1] and V(i) from sv[i&1], and at its start loads
     // K(i+2) into sk[i&1] and V(i+1) into sv[(i+1)&1] (both freed by step
     // i-1), waited for at its closing barrier.
-    dma_k(s_begin, sk0);
-    dma_v(s_begin, sv0);
-    dma_k(s_begin + 1, sk1);
+    dma_k(s_begin, sk0, lane);
+    dma_v(s_begin, sv0, lane);
+    dma_k(s_begin + 1, sk1, lane);
     __syncthreads();
     Scores xa, xb;
     float m_run[2], ms[2], alpha[2] = {1.f, 1.f};
@@ -447,7 +449,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     // is not the block's last part loads one step past its end, never read).  The main loop passes compile-time
     // flags (one straight-line region, buffers known at compile time); the
     // last steps pass runtime flags.
-    auto step_body = [&](auto more, auto mask_next, auto odd, int i, Scores &xc, Scores &xn) {
+    auto step_body = [&](auto more, auto mask_next, auto odd, int i, Scores &xc, Scores &xn, int ln) {
         uint16_t *k_read = odd ? sk0 : sk1;  // K(i+1)
         uint16_t *k_load = odd ? sk1 : sk0;  // K(i+2)
         uint16_t *v_read = odd ? sv1 : sv0;  // V(i)
@@ -462,8 +464,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
                     for (int c = 0; c < 9; ++c) o[ct][c][r] *= a;
                 }
         }
-        if (more && !mask_next) dma_k(s_begin + i + 2, k_load);
-        if (more) dma_v(s_begin + i + 1, v_load);
+        if (more && !mask_next) dma_k(s_begin + i + 2, k_load, ln);
+        if (more) dma_v(s_begin + i + 1, v_load, ln);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) ms[ct] = m_run[ct] * scale;
         half8_t pa[2][2];
@@ -507,11 +509,17 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     const std::integral_constant<bool, false> no;
     int i = 0;
     for (; i + 3 < steps; i += 2) {
-        step_body(yes, no, no, i, xa, xb);
-        step_body(yes, no, yes, i + 1, xb, xa);
+        step_body(yes, no, no, i, xa, xb, lane);
+        step_body(yes, no, yes, i + 1, xb, xa, lane);
     }
+    // The last steps and the epilogue take their lane coordinates from a lane
+    // id computed here (mbcnt), a value the compiler cannot merge with the one
+    // computed before the main loop.  Otherwise it computes their per-lane
+    // addresses before the main loop, where they share the loop's registers
+    // and are spilled around it.
+    const int tail_lane = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
     for (; i < steps; ++i) {  // the last one to three steps
-        step_body(i + 1 < steps, i + 2 == steps && last_part, (i & 1) != 0, i, xa, xb);
+        step_body(i + 1 < steps, i + 2 == steps && last_part, (i & 1) != 0, i, xa, xb, tail_lane);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
@@ -520,6 +528,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
                 for (int e = 0; e < 8; ++e) xa[ct][j][e] = xb[ct][j][e];
     }
 
+    const int lane_e = tail_lane, row_e = tail_lane & 15, kg_e = tail_lane >> 4;
     if (nparts > 1) {
         // Split block: store this part's (m, O, l), count it, and let the part
         // that arrives last merge the other one.  Partials move as 8-byte
@@ -531,10 +540,10 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
         auto slab = [&](uint32_t q) {
             return reinterpret_cast<uint64_t *>(p.partials + (static_cast<size_t>(item) * 2 + q) * kPrefillPartialFloats);
         };
-        auto pair_idx = [&](int ct, int c, int hf) { return (((wave * 2 + ct) * 9 + c) * 2 + hf) * 64 + lane; };
+        auto pair_idx = [&](int ct, int c, int hf) { return (((wave * 2 + ct) * 9 + c) * 2 + hf) * 64 + lane_e; };
         auto m_ptr = [&](uint32_t q, int ct) {
             return p.partials + (static_cast<size_t>(item) * 2 + q) * kPrefillPartialFloats + 4 * 2 * 9 * 4 * 64 +
-                   (wave * 2 + ct) * 64 + lane;
+                   (wave * 2 + ct) * 64 + lane_e;
         };
         {
             uint64_t *own = slab(part);
@@ -553,7 +562,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (threadIdx.x == 0) {
+        if (wave == 0 && lane_e == 0) {
             const uint32_t prev =
                 __hip_atomic_fetch_add(p.counters + item, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             sm_last = prev == nparts - 1;
@@ -581,13 +590,14 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
             m_run[ct] = m_new;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float as = __shfl(a_self, kg * 4 + r);
-                const float ao = __shfl(a_other, kg * 4 + r);
+                const float as = __shfl(a_self, kg_e * 4 + r);
+                const float ao = __shfl(a_other, kg_e * 4 + r);
 #pragma unroll
                 for (int c = 0; c < 9; ++c) o[ct][c][r] = o[ct][c][r] * as + ov[c][r] * ao;
             }
         }
-        if (threadIdx.x == 0) __hip_atomic_store(p.counters + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (wave == 0 && lane_e == 0)
+            __hip_atomic_store(p.counters + item, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // Normalise: output row kg*4 + r of tile ct is query token t0 + kg*4 + r;
@@ -598,11 +608,11 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const float inv = 1.0f / o[ct][8][r];
-            const int t = t0 + kg * 4 + r;
+            const int t = t0 + kg_e * 4 + r;
             if (t < n) {
                 uint16_t *orow = p.out + (static_cast<size_t>(t) * kQueryHeads + h) * kHeadDim;
 #pragma unroll
-                for (int c = 0; c < 8; ++c) orow[c * 16 + row] = __builtin_bit_cast(uint16_t, to_h(o[ct][c][r] * inv));
+                for (int c = 0; c < 8; ++c) orow[c * 16 + row_e] = __builtin_bit_cast(uint16_t, to_h(o[ct][c][r] * inv));
             }
         }
     }

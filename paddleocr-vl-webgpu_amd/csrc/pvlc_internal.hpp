@@ -195,16 +195,32 @@ constexpr uint32_t prefill_pair_segments(uint32_t w, uint32_t qblocks, uint32_t 
     const uint32_t heavy = qblocks - 1u - *pair, light = *pair;
     const uint32_t sh = prefill_block_steps(heavy), sl = light == heavy ? 0u : prefill_block_steps(light);
     const uint32_t k = (sh - sl + 1u) / 2u;  // heavy steps the light block's workgroup takes
-    PrefillSegment *out[2] = {first, second};
+    // Straight-line assignments (no runtime-indexed pointer), so that on the
+    // device both segments stay in registers.  sh >= 1, so k >= sh implies k > 0.
+    PrefillSegment s0{}, s1{};
     uint32_t n = 0;
     if (role == 0) {
-        if (sl) *out[n++] = {light, 0u, 1u, 0u, sl};
-        if (k >= sh) *out[n++] = {heavy, 0u, 1u, 0u, sh};
-        else if (k > 0) *out[n++] = {heavy, 0u, 2u, 0u, k};
-    } else {
-        if (k == 0) *out[n++] = {heavy, 0u, 1u, 0u, sh};
-        else if (k < sh) *out[n++] = {heavy, 1u, 2u, k, sh - k};
+        const PrefillSegment hs = k >= sh ? PrefillSegment{heavy, 0u, 1u, 0u, sh} : PrefillSegment{heavy, 0u, 2u, 0u, k};
+        if (sl) {
+            s0 = {light, 0u, 1u, 0u, sl};
+            n = 1;
+            if (k > 0) {
+                s1 = hs;
+                n = 2;
+            }
+        } else if (k > 0) {
+            s0 = hs;
+            n = 1;
+        }
+    } else if (k == 0) {
+        s0 = {heavy, 0u, 1u, 0u, sh};
+        n = 1;
+    } else if (k < sh) {
+        s0 = {heavy, 1u, 2u, k, sh - k};
+        n = 1;
     }
+    *first = s0;
+    *second = s1;
     return n;
 }
 // Workspace of the pair schedule: an arrival counter per (pair, kv head),
