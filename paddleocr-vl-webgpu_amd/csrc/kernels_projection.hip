@@ -20,7 +20,11 @@
 // 64 x 64 (4 x 4 MFMA tiles of v_mfma_f32_16x16x32_f16 each, hi and lo);
 // operand tiles move by direct global-to-LDS loads through a three-stage
 // ring with one barrier per step.  Every load instruction reads long runs:
-// 1 KiB of the activation block, or 16 weight rows x 64 bytes.
+// 1 KiB of the activation block, or 16 weight rows x 64 bytes.  Projections
+// with at least 512 tiles of 128 x 256 (gate|up at N=4096) run the wide
+// variant instead (kernel 2b below): 4 waves of 64 x 128, and the tiles of
+// each XCD in one block of the output, so both operands are reused from the
+// XCD's L2.
 
 #include <hip/hip_runtime.h>
 
@@ -42,7 +46,7 @@ constexpr int kBlockElems = 2 * kTileElems;  // one activation block: hi and lo 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0, expcnt 6:4, lgkmcnt
 // 11:8, the last two left at their maximum) -- as builtins, so the compiler's
 // own wait insertion knows which loads they retire.
-constexpr int kWaitVm6 = 0x0F76, kWaitVm0 = 0x0F70;  // vmcnt(6) / vmcnt(0)
+constexpr int kWaitVm6 = 0x0F76, kWaitVm4 = 0x0F74, kWaitVm0 = 0x0F70;  // vmcnt(6) / vmcnt(4) / vmcnt(0)
 
 // Exponent e of a row whose largest magnitude is m: m * 2^-e in [2^13, 2^14)
 // (0 for an all-zero row).
@@ -278,6 +282,216 @@ __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_kernel(
     }
 }
 
+// Kernel 2b (wide projections: enough 128 x 256 output tiles to give every
+// compute unit two): projection_gemm_wide_kernel, 128 x 256 output tiles, 4
+// waves of 64 x 128 (4 x 8 MFMA tiles, hi and lo), K in steps of 32.  The activation
+// stages (16 KiB) move through a three-stage ring, loaded two steps ahead,
+// the weight stages (16 KiB) through a two-stage ring, loaded one step ahead:
+// 80 KiB, two workgroups per compute unit (160 KiB of LDS).  Per
+// 32-wide k step a wave reads 8 activation and 8 weight fragments for 64
+// MFMAs, two thirds of the 128 x 128 kernel's LDS reads per MFMA (12 for 32),
+// and a workgroup stores 32 KiB into LDS for twice the products of the 24
+// KiB the narrow kernel stores.
+constexpr int kTileWide = 256;
+constexpr int kWideElems = kTileWide * kTileK;  // one weight stage: 256 rows x 32 k
+constexpr uint32_t kWideResident = 64;          // workgroups one XCD runs at once (32 compute units x 2)
+
+// Tile order of the wide GEMM.  Workgroup b runs on XCD b % 8, so XCD x
+// takes the workgroups b = 8 i + x and, with them, one block of the output:
+// the row tiles split into 8 / col_groups bands and the column tiles into
+// col_groups bands, col_groups chosen by the host to minimise the operand
+// bytes one XCD reads (a row tile's activations and a column tile's weights
+// are the same size).  Inside the block, generations of `gen` columns: all
+// row tiles of the block for columns [g gen, g gen + gen), row-major, so the
+// workgroups resident at once share both operands in the XCD's L2.
+struct WideOrder {
+    uint32_t row_tiles, col_tiles, col_groups, gen;
+};
+
+__device__ inline bool wide_tile(const WideOrder &o, uint32_t b, uint32_t *mt, uint32_t *nt) {
+    const uint32_t x = b % kXcds, idx = b / kXcds;
+    const uint32_t row_groups = kXcds / o.col_groups;
+    const uint32_t xr = x / o.col_groups, xc = x % o.col_groups;
+    const uint32_t r0 = xr * o.row_tiles / row_groups, r1 = (xr + 1) * o.row_tiles / row_groups;
+    const uint32_t c0 = xc * o.col_tiles / o.col_groups, c1 = (xc + 1) * o.col_tiles / o.col_groups;
+    const uint32_t rb = r1 - r0, cb = c1 - c0;
+    if (idx >= rb * cb) return false;
+    const uint32_t gen = o.gen < cb ? o.gen : cb;
+    const uint32_t span = rb * gen, full = cb / gen;
+    uint32_t g, rem, w;
+    if (idx < full * span) {
+        g = idx / span;
+        rem = idx % span;
+        w = gen;
+    } else {
+        g = full;
+        rem = idx - full * span;
+        w = cb - full * gen;
+    }
+    *mt = r0 + rem / w;
+    *nt = c0 + g * gen + rem % w;
+    return true;
+}
+
+__global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_wide_kernel(
+    const uint16_t *__restrict__ tiles, const int32_t *__restrict__ exponents, const uint16_t *__restrict__ weight,
+    const float *__restrict__ bias, float *__restrict__ out, uint32_t rows, uint32_t k_width, uint32_t n_width,
+    WideOrder order) {
+    uint32_t mt, nt;
+    if (!wide_tile(order, blockIdx.x, &mt, &nt)) return;  // uniform: a smaller block of this XCD
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int row16 = lane & 15, kg = lane >> 4;
+    const uint32_t m0 = mt * kTileM, n0 = nt * kTileWide;
+    const int wm = wave >> 1, wn = wave & 1;  // the wave's 64 x 128 part: rows wm * 64, columns wn * 128
+    const uint32_t steps = k_width / kTileK;
+
+    // The stages as distinct arrays, picked at compile time by the loop
+    // unrolled by six (the period of the two rings).
+    __shared__ uint16_t sa0[kBlockElems], sa1[kBlockElems], sa2[kBlockElems];
+    __shared__ uint16_t sw0[kWideElems], sw1[kWideElems];
+    typedef __attribute__((address_space(3))) void *lds_ptr;
+
+    // Direct global-to-LDS loads, 1 KiB per instruction: activations as in
+    // the narrow kernel (4 per wave); weights 16 instructions of 16 rows, 4
+    // per wave, lane l of instruction j filling LDS slot p = 64 j + l (row p /
+    // 4, slot p % 4, the row's k-chunk slot ^ ((row / 2) % 4)).  Weight rows
+    // past the end re-read the last row (never stored).
+    const uint16_t *a_tiles = tiles + static_cast<size_t>(mt) * steps * kBlockElems + (wave * 4) * 512 + lane * 8;
+    const uint32_t last_col = n_width - 1;
+    size_t w_row_off[4];
+#pragma unroll
+    for (int rw = 0; rw < 4; ++rw) {
+        const int p = 64 * (wave * 4 + rw) + lane, wrow = p >> 2;
+        const int kc = (p & 3) ^ ((wrow >> 1) & 3);
+        w_row_off[rw] = static_cast<size_t>(min(n0 + wrow, last_col)) * k_width + kc * 8;
+    }
+    auto load_a = [&](uint32_t s, uint16_t *da) {
+        const uint16_t *a = a_tiles + static_cast<size_t>(s) * kBlockElems;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            __builtin_amdgcn_global_load_lds(a + j * 512, (lds_ptr)(da + (wave * 4 + j) * 512), 16, 0, 0);
+    };
+    auto load_w = [&](uint32_t s, uint16_t *dw) {
+#pragma unroll
+        for (int rw = 0; rw < 4; ++rw)
+            __builtin_amdgcn_global_load_lds(weight + w_row_off[rw] + s * kTileK,
+                                             (lds_ptr)(dw + (wave * 4 + rw) * 512), 16, 0, 0);
+    };
+
+    float4_t acc[4][8];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // The fragment layouts of the narrow kernel: A = activations (lane row
+    // l % 16, k (l / 16) * 8 ..), B = W^T (lane column l % 16, same k).
+    auto compute = [&](const uint16_t *sa, const uint16_t *sw) {
+        half8_t bf[8];
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb)
+            bf[cb] = *reinterpret_cast<const half8_t *>(sw + w_offset(kg, wn * 128 + cb * 16 + row16));
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            const int trow = wm * 64 + rb * 16 + row16;
+            const half8_t ah = *reinterpret_cast<const half8_t *>(sa + a_offset(kg, trow));
+            const half8_t al = *reinterpret_cast<const half8_t *>(sa + kTileElems + a_offset(kg, trow));
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb)
+                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bf[cb], acc[rb][cb], 0, 0, 0);
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb)
+                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[cb], acc[rb][cb], 0, 0, 0);
+        }
+        // Schedule: the weight fragments and the first row block's first,
+        // then each row block's 16 MFMAs with the next row block's two
+        // fragment reads issued after its first MFMA and the step's 8
+        // global-to-LDS loads spread among them (masks: 0x100 LDS read,
+        // 0x008 MFMA, 0x020 global load).  Measured against the compiler's own
+        // order (a wait for each row block's reads): gate|up 138 -> 127 us.
+        __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (rb < 3) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+        }
+    };
+    // Step s: wait until at most the 4 activation loads of stage s + 1 are
+    // outstanding (this wave's loads of the activations and weights of stage
+    // s have landed), barrier (every wave's have, and every wave has finished
+    // reading the buffers of stage s - 1), load the weights of stage s + 1
+    // and then the activations of stage s + 2 into those buffers (past the
+    // end: the last stage again, never read), compute stage s.  Unconditional
+    // loads keep the waits exact.
+    auto step = [&](uint32_t s, uint16_t *ca, uint16_t *cw, uint16_t *na2, uint16_t *nw1) {
+        __builtin_amdgcn_s_waitcnt(kWaitVm4);
+        __builtin_amdgcn_s_barrier();
+        load_w(min(s + 1, steps - 1), nw1);
+        load_a(min(s + 2, steps - 1), na2);
+        compute(ca, cw);
+    };
+
+    load_a(0, sa0);
+    load_w(0, sw0);
+    load_a(min(1u, steps - 1), sa1);
+    uint32_t s = 0;
+    for (; s + 6 <= steps; s += 6) {
+        step(s, sa0, sw0, sa2, sw1);
+        step(s + 1, sa1, sw1, sa0, sw0);
+        step(s + 2, sa2, sw0, sa1, sw1);
+        step(s + 3, sa0, sw1, sa2, sw0);
+        step(s + 4, sa1, sw0, sa0, sw1);
+        step(s + 5, sa2, sw1, sa1, sw0);
+    }
+    if (s < steps) step(s, sa0, sw0, sa2, sw1);
+    if (s + 1 < steps) step(s + 1, sa1, sw1, sa0, sw0);
+    if (s + 2 < steps) step(s + 2, sa2, sw0, sa1, sw1);
+    if (s + 3 < steps) step(s + 3, sa0, sw1, sa2, sw0);
+    if (s + 4 < steps) step(s + 4, sa1, sw0, sa0, sw1);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // no load into LDS outlives the loop
+
+    // Epilogue: x 2^e of the row (exact), + bias, f32 stores.
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = m0 + wm * 64 + rb * 16 + kg * 4 + i;
+            if (r >= rows) continue;
+            const int e = exponents[r];
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb) {
+                const uint32_t n = n0 + wn * 128 + cb * 16 + row16;
+                if (n < n_width) out[static_cast<size_t>(r) * n_width + n] = __builtin_ldexpf(acc[rb][cb][i], e) + bias[n];
+            }
+        }
+    }
+}
+
+// Order of the wide GEMM's tiles for rows x n_width: the column grouping that
+// minimises the operand bytes of the largest XCD block, and generations of
+// columns sized so that one generation is what an XCD runs at once.
+WideOrder wide_order(uint32_t row_tiles, uint32_t col_tiles) {
+    WideOrder best{row_tiles, col_tiles, 1, 1};
+    uint32_t best_cost = UINT32_MAX;
+    for (uint32_t gc = 1; gc <= kXcds; gc *= 2) {
+        const uint32_t gr = kXcds / gc;
+        const uint32_t rb = (row_tiles + gr - 1) / gr, cb = (col_tiles + gc - 1) / gc;
+        if (rb + cb < best_cost) {
+            best_cost = rb + cb;
+            best.col_groups = gc;
+        }
+    }
+    const uint32_t rb = (row_tiles + kXcds / best.col_groups - 1) / (kXcds / best.col_groups);
+    best.gen = kWideResident / rb > 0 ? kWideResident / rb : 1;
+    return best;
+}
+
 }  // namespace
 
 int launch_linear_projection_f16(const float *input, const uint16_t *weight, const float *bias, float *out,
@@ -294,6 +508,19 @@ int launch_linear_projection_f16(const float *input, const uint16_t *weight, con
     default: hipLaunchKernelGGL(projection_split_kernel<0>, split_grid, dim3(kSplitThreads), 0, st, input, rows, k_width, ws.tiles, ws.exponents); break;
     }
     if (hipError_t e = hipGetLastError()) return static_cast<int>(e);
+    const uint32_t wide_cols = n_width / kTileWide + (n_width % kTileWide != 0);
+    if (static_cast<uint64_t>(wide_cols) * m_tiles >= 2 * kTargetWorkgroups) {
+        // Enough wide tiles for two workgroups on every compute unit: the
+        // wide kernel (with fewer, its second slot on most compute units
+        // stays empty, and the narrow kernel's twice as many tiles finish
+        // sooner: q|k|v at N=4096, 320 wide tiles, 80 us against 72).
+        const WideOrder order = wide_order(m_tiles, wide_cols);
+        const uint32_t row_groups = kXcds / order.col_groups;
+        const uint32_t block = ((m_tiles + row_groups - 1) / row_groups) * ((wide_cols + order.col_groups - 1) / order.col_groups);
+        hipLaunchKernelGGL(projection_gemm_wide_kernel, dim3(kXcds * block), dim3(kGemmThreads), 0, st, ws.tiles,
+                           ws.exponents, weight, bias, out, rows, k_width, n_width, order);
+        return static_cast<int>(hipGetLastError());
+    }
     const uint32_t tiles = (n_width / kTileN + (n_width % kTileN != 0)) * m_tiles;  // < 2^24 (checked by the caller)
     hipLaunchKernelGGL(projection_gemm_kernel, dim3(tiles), dim3(kGemmThreads), 0, st, ws.tiles, ws.exponents, weight,
                        bias, out, rows, k_width, n_width);
