@@ -288,7 +288,7 @@ def measure_config2(pvlc, torch, args):
 # Read-probe shapes (workgroups, waves, KiB per wave): the config-2 decode grid as launched (216 workgroups of 12
 # waves, 16 KiB each: the 37.75 MiB of keys and values plus the re-reads of short last partitions), then
 # 37.75 MiB exactly under other grids.
-READ_FLOOR_SHAPES = ((216, 12, 16), (288, 8, 16), (144, 16, 16), (576, 4, 16), (1152, 4, 8), (144, 8, 32),
+READ_FLOOR_SHAPES = ((252, 10, 16), (216, 12, 16), (288, 8, 16), (144, 16, 16), (576, 4, 16), (1152, 4, 8), (144, 8, 32),
                      (256, 12, 8), (512, 12, 8))
 
 

@@ -38,8 +38,8 @@ __global__ __launch_bounds__(WAVES * 64) void hbm_read_kernel(const u32x4 *src, 
 }  // namespace
 
 // Bytes one launch reads: workgroups * waves * loads KiB.  waves in {4, 8, 12,
-// 16}, loads in {8, 16, 32}; returns 0, the launch's hipError_t, or -1 for
-// another shape.
+// 16} with loads in {8, 16, 32}, or 10 waves of 16; returns 0, the launch's
+// hipError_t, or -1 for another shape.
 extern "C" int pvlc_probe_hbm_read(const void *src, uint32_t *sink, uint32_t workgroups, uint32_t waves,
                                    uint32_t loads, uint32_t never, void *stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -56,6 +56,7 @@ extern "C" int pvlc_probe_hbm_read(const void *src, uint32_t *sink, uint32_t wor
     PVLC_PROBE(8, 8)
     PVLC_PROBE(8, 16)
     PVLC_PROBE(8, 32)
+    PVLC_PROBE(10, 16)
     PVLC_PROBE(12, 8)
     PVLC_PROBE(12, 16)
     PVLC_PROBE(12, 32)
