@@ -534,7 +534,7 @@ def batched_cpu_baseline(pvlc, torch, plane, d_tables, num_blocks, lens, q, out,
             "gbps": round(step_bytes / per_step / 1e9, 3),
             "sample": f"{reps} x decode_gqa_f32 of {len(rows)} sequences ({sample_rows} rows), scaled by the "
                       f"batch's {int(lens.sum())} rows ({elapsed:.1f} s)",
-            "gpu_vs_cpu_max_abs": max_abs}
+            "host": host_cpu_info(), "gpu_vs_cpu_max_abs": max_abs}
 
 
 def bench_prefill(args):
@@ -625,7 +625,7 @@ def prefill_cpu_baseline(pvlc, torch, n, nb, q, kp, vp, out, seconds, flops, sam
             "tflops": round(flops / per_call / 1e12, 6),
             "sample": f"{reps} x {sample} query rows (decode over keys 0..i, {sampled} attended rows), scaled to "
                       f"N(N+1)/2 = {n * (n + 1) // 2} ({elapsed:.1f} s)",
-            "gpu_vs_cpu_max_abs": max_abs}
+            "host": host_cpu_info(), "gpu_vs_cpu_max_abs": max_abs}
 
 
 # Decoder projections of one layer, rows x columns (gemv_tiled_plan_contract.rs and
@@ -1088,7 +1088,7 @@ def projection_cpu_baseline(calls, n, seconds, layer_flops, sample_rows=16):
     return {"value": round(per_layer * 1e6, 1), "unit": "µs/layer", "cores": 1, "kind": "port",
             "tflops": round(layer_flops / per_layer / 1e12, 6),
             "sample": f"{reps} x first {sample_rows} rows of the 4 projections, scaled to N={n} ({elapsed:.1f} s)",
-            "gpu_vs_cpu_max_rel": max_rel}
+            "host": host_cpu_info(), "gpu_vs_cpu_max_rel": max_rel}
 
 
 def gemv_cpu_baseline(calls, logits, seconds, step_bytes):
@@ -1120,7 +1120,7 @@ def gemv_cpu_baseline(calls, logits, seconds, step_bytes):
             "gbps": round(step_bytes / per_step / 1e9, 3),
             "sample": f"{reps} x (one layer's 7 GEMVs + LM head), scaled to 18 layers + head "
                       f"({layer_t + head_t:.1f} s)",
-            "gpu_vs_cpu_logits_max_abs": max_err}
+            "host": host_cpu_info(), "gpu_vs_cpu_logits_max_abs": max_err}
 
 
 def cpu_baseline(host_q, host_k, host_v, host_nk, host_nv, cos, sin, seconds, step_bytes, gpu_out):
@@ -1151,20 +1151,41 @@ def cpu_baseline(host_q, host_k, host_v, host_nk, host_nv, cos, sin, seconds, st
     per_step = elapsed / steps
     gpu = gpu_out.float().cpu().numpy().reshape(LAYERS, 2048)
     max_err = float(np.max(np.abs(gpu - np.stack(outs))))
-    model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {"value": round(per_step * 1e6, 1), "unit": "µs/step", "cores": 1, "kind": "port",
             "gbps": round(step_bytes / per_step / 1e9, 3),
             "sample": f"{steps} full 18-layer steps at T=2048 on replica 0 ({elapsed:.1f} s)",
-            "host": {"nproc": os.cpu_count(), "cpu": model},
+            "host": host_cpu_info(),
             "gpu_vs_cpu_max_abs": max_err}
+
+
+def host_cpu_info():
+    """The host the CPU baseline ran on: lscpu's model name (else /proc/cpuinfo's), the CPUs the process may
+    run on, and the threads the baseline used (one: the reference crate has no threading)."""
+    import subprocess
+
+    model, source = "unknown", None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model, source = line.split(":", 1)[1].strip(), "lscpu"
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if source is None:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        model, source = line.split(":", 1)[1].strip(), "/proc/cpuinfo"
+                        break
+        except OSError:
+            pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"nproc": usable, "cpu_count": os.cpu_count(), "cpu": model, "cpu_source": source, "threads_used": 1}
 
 
 if __name__ == "__main__":
