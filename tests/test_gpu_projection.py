@@ -97,3 +97,32 @@ def test_rows_far_outside_the_fp16_range_keep_f32_accuracy():
     got, wf, xx, b = run_projection(rows, k, n, seed=77, x=x, zero_bias=True)
     check(rows, k, n, got, wf, xx, b, "dynamic range")
     np.testing.assert_array_equal(got[2], b)
+
+
+@pytest.mark.parametrize("rows,k,n", [(4096, 1024, 6144),   # gate|up at N=4096: 768 wide tiles, 2 generations per XCD
+                                      (2049, 256, 7940),    # ragged rows and columns: uneven XCD blocks
+                                      (1100, 96, 16384)])   # 3 k steps: the ring's tail without a full period
+def test_wide_kernel_writes_every_tile(rows, k, n):
+    """Shapes with at least 512 tiles of 128 x 256 run the wide GEMM, whose tiles each XCD takes in one block of
+    the output: every output element is written (the output starts as NaN) and two rows of every 128-row tile
+    (its first and last) are within the f64 bound over all columns."""
+    import torch
+    log(f"case: wide projection rows={rows} k={k} n={n}")
+    seed = rows + k + n
+    w = f16_bits(seed, n * k, 0.05)
+    x = O.normal_f32(seed + 1, rows * k).reshape(rows, k)
+    b = O.normal_f32(seed + 2, n)
+    wsb = pvlc.linear_projection_workspace_bytes(rows, k)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    d_out = torch.full((rows * n + 64,), float("nan"), dtype=torch.float32, device="cuda")
+    pvlc.linear_projection_f16(to_dev_f32(x), to_dev(w), to_dev_f32(b), d_out, rows, k, n, ws, wsb)
+    torch.cuda.synchronize()
+    got = d_out.cpu().numpy()
+    assert np.all(np.isnan(got[rows * n:])), "projection wrote past the output"
+    got = got[:rows * n].reshape(rows, n)
+    assert np.all(np.isfinite(got)), f"{int(np.sum(~np.isfinite(got)))} outputs never written"
+    sel = sorted({r for t in range(0, rows, 128) for r in (t, min(t + 127, rows - 1))})
+    wf = widen(w).reshape(n, k)
+    ratio = bound_ratio(got[sel], wf, x[sel], b, 2 * k + 2, True)
+    log(f"[parity] wide projection {rows}x{k}x{n}: {len(sel)} rows, max |gpu - f64| / bound = {ratio:.3f}")
+    assert ratio <= 1.0
