@@ -75,6 +75,8 @@ def parse():
                     help="prefill projections of one decoder layer at N=4096 (fp16 weights, f32 activations)")
     ap.add_argument("--gemv", action="store_true",
                     help="decoder weight GEMVs of one token step (18 layers x 7 projections + LM head, fp16 weights)")
+    ap.add_argument("--chain", action="store_true",
+                    help="the decoder token step alone (18 layers of GEMVs and single-layer decodes + LM head top-1)")
     return ap.parse_args()
 
 
@@ -92,6 +94,12 @@ def main() -> int:
         return bench_gemv(args)
     if args.projection:
         return bench_projection(args)
+    if args.chain:
+        import torch
+
+        from __graft_entry__ import load_package
+        print(json.dumps({"decoder_token_step": bench_token_chain(load_package(), torch, args)}, ensure_ascii=False))
+        return 0
     if args.config == 4:
         return bench_prefill(args)
     if args.config in (3, 5):
@@ -798,10 +806,9 @@ class TokenChain:
     on this backend's entry points, for `layers` layers at `context` rows attended after the append:
 
         per layer: q|k|v  = grouped GEMV (pvlc_hip_gemv_group_f16) of the hidden state x   (f32 out)
-                   q|k|v -> fp16                                                            (torch copy)
-                   attn   = pvlc_hip_paged_decode_f16 over the layer's cache, num_seqs = 1: rotary on q and
-                            the new key, append at row context-1, GQA over `context` rows  (fp16 out)
-                   attn  -> f32                                                             (torch copy)
+                   attn   = pvlc_hip_paged_decode_f32io over the layer's cache, num_seqs = 1: rotary on q
+                            and the new key, append at row context-1, GQA over `context` rows
+                            (f32 operands in and out, as the reference's chain passes them)
                    o      = GEMV o (1024 x 2048)
                    g|u    = grouped GEMV gate|up (3072 x 1024 each) of o
                    x'     = GEMV down (1024 x 3072) of g
@@ -810,12 +817,16 @@ class TokenChain:
     The decoder's norms, residual adds and SwiGLU are outside this backend and left out (down reads the gate
     output directly); the data dependencies between layers are the decoder's.  Weights are seeded N(0,1)*0.02
     fp16, caches N(0,1) fp16, each layer its own; per-layer q|k|v and attention outputs stay in their own
-    buffers so a test can check every layer."""
+    buffers so a test can check every layer.
 
-    def __init__(self, pvlc, torch, layers, context, capacity, head_rows, seed=21):
+    f32_operands=False runs the fp16 entry point pvlc_hip_paged_decode_f16 instead, with a torch conversion of
+    q|k|v to fp16 before it and of its fp16 output to f32 after it (two more launches per layer)."""
+
+    def __init__(self, pvlc, torch, layers, context, capacity, head_rows, seed=21, f32_operands=True):
         dev = torch.device("cuda:0")
         gen = torch.Generator(device=dev).manual_seed(seed)
         self.pvlc, self.torch, self.layers, self.context, self.head_rows = pvlc, torch, layers, context, head_rows
+        self.f32_operands = f32_operands
         self.nb = (capacity + 15) // 16
         plane = layers * self.nb * 16 * W
 
@@ -833,7 +844,7 @@ class TokenChain:
         self.qkv32 = [torch.empty(2560, device=dev) for _ in range(layers)]
         self.qkv16 = [torch.empty(2560, dtype=torch.float16, device=dev) for _ in range(layers)]
         self.attn16 = [torch.empty(2048, dtype=torch.float16, device=dev) for _ in range(layers)]
-        self.attn32 = torch.empty(2048, device=dev)
+        self.attn32 = [torch.empty(2048, device=dev) for _ in range(layers if f32_operands else 1)]
         self.o32 = torch.empty(1024, device=dev)
         self.gu32 = torch.empty(6144, device=dev)
         self.logits = torch.empty(head_rows, device=dev)
@@ -856,21 +867,36 @@ class TokenChain:
                                                      (self.w[l]["up"], self.gu32[3072:], 3072)]))
             off = l * self.nb * 16 * W
             q16 = self.qkv16[l]
+            fp16 = not f32_operands
             self.decode_args.append(pvlc.paged_decode_args(
                 num_seqs=1, num_blocks=self.nb, max_blocks_per_seq=self.nb, key_cache=self.kp[off:],
-                value_cache=self.vp[off:], query=q16[:2048], new_key=q16[2048:2304], new_value=q16[2304:],
-                out=self.attn16[l], workspace=self.ws, workspace_bytes=self.wsb, max_context=capacity,
-                uniform_cache_len=context - 1, rope_cos=self.cos, rope_sin=self.sin, rope_rows=capacity,
-                rotate_query=True))
+                value_cache=self.vp[off:], query=q16[:2048] if fp16 else None,
+                new_key=q16[2048:2304] if fp16 else None, new_value=q16[2304:] if fp16 else None,
+                out=self.attn16[l] if fp16 else None, workspace=self.ws, workspace_bytes=self.wsb,
+                max_context=capacity, uniform_cache_len=context - 1, rope_cos=self.cos, rope_sin=self.sin,
+                rope_rows=capacity, rotate_query=True))
         torch.cuda.synchronize()
+
+    def attention(self, l, st):
+        """Layer l's decode on the q|k|v its projections wrote."""
+        if self.f32_operands:
+            q = self.qkv32[l]
+            self.pvlc.paged_decode_f32io(self.decode_args[l], q[:2048], q[2048:2304], q[2304:], self.attn32[l], st)
+        else:
+            self.pvlc.paged_decode_f16(self.decode_args[l], st)
 
     def layer(self, l, st):
         pvlc = self.pvlc
         pvlc.gemv_group_f16(self.qkv_members[l], self.xs[l], 1024, st)
-        self.qkv16[l].copy_(self.qkv32[l])
-        pvlc.paged_decode_f16(self.decode_args[l], st)
-        self.attn32.copy_(self.attn16[l])
-        pvlc.gemv_f16(self.w[l]["o"], self.attn32, self.o32, 1024, 2048, st)
+        if self.f32_operands:
+            self.attention(l, st)
+            attn = self.attn32[l]
+        else:
+            self.qkv16[l].copy_(self.qkv32[l])
+            self.attention(l, st)
+            attn = self.attn32[0]
+            attn.copy_(self.attn16[l])
+        pvlc.gemv_f16(self.w[l]["o"], attn, self.o32, 1024, 2048, st)
         pvlc.gemv_group_f16(self.gu_members[l], self.o32, 1024, st)
         pvlc.gemv_f16(self.w[l]["down"], self.gu32[:3072], self.xs[l + 1], 1024, 3072, st)
 
@@ -884,7 +910,7 @@ class TokenChain:
     def attention_only(self, st):
         """The 18 single-layer decode launches alone (the step's attention part)."""
         for l in range(self.layers):
-            self.pvlc.paged_decode_f16(self.decode_args[l], st)
+            self.attention(l, st)
 
     def capture(self, fn):
         """Capture fn(stream) into a HIP graph on a side stream after one warm-up run there."""
@@ -903,15 +929,16 @@ class TokenChain:
 
     def state(self):
         """Every buffer the step writes (for bit-exact comparisons)."""
-        return ([t.clone() for t in self.xs[1:]] + [t.clone() for t in self.qkv16] + [t.clone() for t in self.attn16]
+        per_layer = self.attn32 if self.f32_operands else self.qkv16 + self.attn16
+        return ([t.clone() for t in self.xs[1:]] + [t.clone() for t in self.qkv32] + [t.clone() for t in per_layer]
                 + [self.logits.clone(), self.result.clone()])
 
 
-def bench_token_chain(pvlc, torch, args):
-    """The 18-layer decoder token step at T=2048 (TokenChain) replayed from a HIP graph, its attention launches
-    alone, and the same step launched eagerly; the first replay is checked against the eager step bit for bit."""
+def _measure_chain(pvlc, torch, args, f32_operands):
+    """One TokenChain: the step replayed from a HIP graph (the first replay checked bit for bit against the eager
+    step), its attention launches alone, and the step launched eagerly."""
     stream = torch.cuda.current_stream()
-    chain = TokenChain(pvlc, torch, LAYERS, CONTEXT, CAPACITY, GEMV_HEAD[1])
+    chain = TokenChain(pvlc, torch, LAYERS, CONTEXT, CAPACITY, GEMV_HEAD[1], f32_operands=f32_operands)
     chain.step(stream)
     torch.cuda.synchronize()
     eager = chain.state()
@@ -928,13 +955,23 @@ def bench_token_chain(pvlc, torch, args):
     stats = _launch_stats(torch, stream, steps, lambda i: graph.replay())
     ms_att = _timed_launches(torch, stream, steps, lambda i: att_graph.replay())
     ms_eager = _timed_launches(torch, stream, min(steps, 20), lambda i: chain.step(stream))
+    del chain, graph, att_graph
+    return ms_step, stats, ms_att, ms_eager
+
+
+def bench_token_chain(pvlc, torch, args):
+    """The 18-layer decoder token step at T=2048 (TokenChain, f32 operands between the stages as in the reference's
+    chain) replayed from a HIP graph, its attention launches alone, and the same step launched eagerly; beside it
+    the step with the fp16 decode entry point and its two conversions per layer."""
+    ms_step, stats, ms_att, ms_eager = _measure_chain(pvlc, torch, args, True)
+    ms16_step, stats16, ms16_att, _ = _measure_chain(pvlc, torch, args, False)
     weight_bytes = sum(gemv_bytes(r, c) for _, r, c in GEMV_LAYER) * LAYERS + gemv_bytes(GEMV_HEAD[1], GEMV_HEAD[2])
     att_bytes = LAYERS * algorithmic_bytes(CONTEXT)
-    return {"workload": "one decoder token step at T=2048: 18 layers x (grouped q|k|v GEMV, fp16 conversion, "
-                        "single-layer paged decode with rotary q/k, append and GQA, f32 conversion, o GEMV, grouped "
-                        "gate|up GEMV, down GEMV) + LM head 103424x1024 fused with greedy top-1; norms and SwiGLU "
-                        "left out (outside this backend)",
-            "launches_per_step": LAYERS * 7 + 2,
+    return {"workload": "one decoder token step at T=2048: 18 layers x (grouped q|k|v GEMV, single-layer paged decode "
+                        "with rotary q/k, append and GQA on f32 operands, o GEMV, grouped gate|up GEMV, down GEMV) + "
+                        "LM head 103424x1024 fused with greedy top-1; norms and SwiGLU left out (outside this "
+                        "backend)",
+            "launches_per_step": LAYERS * 5 + 2,
             "graph_us_per_token": round(ms_step * 1e3, 2), "graph_spread": stats,
             "eager_us_per_token": round(ms_eager * 1e3, 2),
             "attention_per_layer_us": round(ms_att * 1e3 / LAYERS, 3),
@@ -943,7 +980,13 @@ def bench_token_chain(pvlc, torch, args):
                               "graph back to back; config 2's headline runs the same 18 layers as one launch",
             "bytes_per_token": weight_bytes + att_bytes,
             "gbps": round((weight_bytes + att_bytes) / (ms_step * 1e-3) / 1e9, 1),
-            "replay_bit_exact_vs_eager": True}
+            "replay_bit_exact_vs_eager": True,
+            "with_fp16_decode_operands": {
+                "note": "pvlc_hip_paged_decode_f16 with a torch conversion of q|k|v to fp16 before it and of its "
+                        "output to f32 after it",
+                "launches_per_step": LAYERS * 7 + 2,
+                "graph_us_per_token": round(ms16_step * 1e3, 2), "graph_spread": stats16,
+                "attention_per_layer_us": round(ms16_att * 1e3 / LAYERS, 3)}}
 
 
 def _gemv_graph(torch, step, calls):

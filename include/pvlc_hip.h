@@ -406,6 +406,19 @@ pvlc_hip_status pvlc_hip_workspace_error(const void *workspace, size_t workspace
  * decoder_gqa_split_merge_f32 (pvlc-wgsl lib.rs:927-952, 1024-1234; issued by
  * pvlc-runtime-web decoder_stack_session.rs:4698-4729) with one launch. */
 pvlc_hip_status pvlc_hip_paged_decode_f16(const pvlc_hip_paged_decode_args *args, void *stream);
+/* The same step with the per-token operands in f32, as the reference's chain
+ * passes them between its dispatches (decoder_mrope_f32 reads the f32 q/k/v
+ * its projections wrote, decoder_gqa_split_merge_f32 writes the f32 attention
+ * output the o projection reads; pvlc-wgsl lib.rs:1024-1234, web
+ * decoder_stack_session.rs:4698-4729): query [num_seqs][16][128], new_key and
+ * new_value [num_seqs][2][128], out [num_seqs][16][128], all f32 device
+ * pointers.  The query and the new key are rotated from their f32 values and
+ * rounded to fp16 once (RNE); the new value is rounded to fp16; the cache
+ * stays fp16; the output is the f32 quotient the fp16 entry point rounds.
+ * args->query, new_key, new_value and out must be NULL; everything else as
+ * pvlc_hip_paged_decode_f16. */
+pvlc_hip_status pvlc_hip_paged_decode_f32io(const pvlc_hip_paged_decode_args *args, const float *query,
+                                            const float *new_key, const float *new_value, float *out, void *stream);
 
 /* pvlc_hip_paged_decode_f16 without allocation: the same validation, kernels
  * and results (bit-identical outputs and caches), with the split-K state kept

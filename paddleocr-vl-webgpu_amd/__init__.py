@@ -208,6 +208,7 @@ SIGNATURES = {
     "pvlc_hip_workspace_error": ([_VP, _SZ, _VP, ctypes.POINTER(_U32)], ctypes.c_int32),
     "pvlc_hip_paged_decode_f16": ([ctypes.POINTER(PagedDecodeArgsC), _VP], ctypes.c_int32),
     "pvlc_hip_paged_decode_f16_no_alloc": ([ctypes.POINTER(PagedDecodeArgsC), _VP, _VP], ctypes.c_int32),
+    "pvlc_hip_paged_decode_f32io": ([ctypes.POINTER(PagedDecodeArgsC), _VP, _VP, _VP, _VP, _VP], ctypes.c_int32),
     "pvlc_hip_paged_prefill_f16": ([ctypes.POINTER(PagedPrefillArgsC), _VP], ctypes.c_int32),
     "pvlc_hip_kv_pack_f16": ([_VP, _VP, _U32, _VP, _U32, _VP, _VP, _VP], ctypes.c_int32),
     "pvlc_hip_kv_unpack_f16": ([_VP, _VP, _U32, _VP, _U32, _VP, _VP, _VP], ctypes.c_int32),
@@ -722,6 +723,13 @@ def paged_decode_f16(args: PagedDecodeArgsC, stream=None) -> None:
     """One fused rotary+append+attention decode step for every sequence
     (replaces decoder_mrope/kv_append/gqa_split_partial/merge, wgsl lib.rs:927-1234)."""
     _check(lib.pvlc_hip_paged_decode_f16(ctypes.byref(args), _stream(stream)))
+
+
+def paged_decode_f32io(args: PagedDecodeArgsC, query, new_key, new_value, out, stream=None) -> None:
+    """paged_decode_f16 with f32 query, new key and value and output, the reference chain's operand format
+    (the args' fp16 operand pointers must be None)."""
+    _check(lib.pvlc_hip_paged_decode_f32io(ctypes.byref(args), _ptr(query), _ptr(new_key), _ptr(new_value),
+                                           _ptr(out), _stream(stream)))
 
 
 def paged_decode_f16_no_alloc(args: PagedDecodeArgsC, error_word, stream=None) -> None:

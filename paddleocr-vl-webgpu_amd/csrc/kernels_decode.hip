@@ -65,6 +65,12 @@ struct DecodeParams {
     uint32_t *partition_word;  // streaming, automatic partition: the one used (else null)
     uint32_t compute_units;    // streaming: compute units of the device
     float scale_log2;   // log2(e)/sqrt(128)
+    // f32 operands (pvlc_hip_paged_decode_f32io): query, new key and value,
+    // output; null for the fp16 entry points.
+    const float *query32;
+    const float *new_key32;
+    const float *new_value32;
+    float *out32;
 };
 
 // Block ids of every tile this wave loads in one partition, one per lane:
@@ -134,7 +140,7 @@ __device__ inline void load_chunk(const DecodeParams &p, uint32_t g, uint32_t id
 // the workgroup.  Errors are
 // reported after the key/value loads are consumed, so no conditional memory
 // operation sits among them.
-template <int WAVES, int PAIRS, bool DEFER_MERGE>
+template <int WAVES, int PAIRS, bool DEFER_MERGE, bool F32IO>
 __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uint32_t g, uint32_t part, int cache_len,
                                    int pos, uint32_t ids, bool ids_bad) {
     constexpr int kChunkTiles = 2 * PAIRS;         // 16-token tiles a wave holds in registers at once
@@ -164,21 +170,52 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     // column = query head of the group (8 real, 8 zero), k = dims
     // kb*32 + kg*8 .. +8 (lanes of the zero columns load a real row and
     // discard it).
-    const uint16_t *qrow = p.query + (static_cast<size_t>(s) * kQueryHeads + g * kGroup + (row & 7)) * kHeadDim;
+    // With f32 operands the query is kept as given until it is rotated, and
+    // rounded to fp16 once (RNE), as the new key below.
+    const size_t qoff = (static_cast<size_t>(s) * kQueryHeads + g * kGroup + (row & 7)) * kHeadDim;
     half8_t qb[4];
+    float qf[F32IO ? 4 : 1][8];
+    if constexpr (F32IO) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) qb[kb] = *reinterpret_cast<const half8_t *>(qrow + kb * 32 + kg * 8);
+        for (int kb = 0; kb < 4; ++kb) {
+            const float4_t lo = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8);
+            const float4_t hi = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8 + 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                qf[kb][j] = lo[j];
+                qf[kb][j + 4] = hi[j];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qb[kb][j] = to_h(qf[kb][j]);
+        }
+    } else {
+        const uint16_t *qrow = p.query + qoff;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) qb[kb] = *reinterpret_cast<const half8_t *>(qrow + kb * 32 + kg * 8);
+    }
     // The appended row and the rotary row at its position: lane t holds
     // dims t and t+64 (the rotate-half pair) and cos/sin of pair t.
     const size_t new_base = (static_cast<size_t>(s) * kKvHeads + g) * kHeadDim;
-    const uint16_t nk_lo = p.new_key[new_base + lane];
-    const uint16_t nk_hi = p.new_key[new_base + lane + 64];
-    const uint16_t nv_lo = p.new_value[new_base + lane];
-    const uint16_t nv_hi = p.new_value[new_base + lane + 64];
+    uint16_t nk_lo, nk_hi, nv_lo, nv_hi;
+    float nkf_lo = 0.f, nkf_hi = 0.f;  // f32 operands: the new key before its rotation and rounding
+    if constexpr (F32IO) {
+        nkf_lo = p.new_key32[new_base + lane];
+        nkf_hi = p.new_key32[new_base + lane + 64];
+        nk_lo = __builtin_bit_cast(uint16_t, to_h(nkf_lo));
+        nk_hi = __builtin_bit_cast(uint16_t, to_h(nkf_hi));
+        nv_lo = __builtin_bit_cast(uint16_t, to_h(p.new_value32[new_base + lane]));
+        nv_hi = __builtin_bit_cast(uint16_t, to_h(p.new_value32[new_base + lane + 64]));
+    } else {
+        nk_lo = p.new_key[new_base + lane];
+        nk_hi = p.new_key[new_base + lane + 64];
+        nv_lo = p.new_value[new_base + lane];
+        nv_hi = p.new_value[new_base + lane + 64];
+    }
     // (Without rotary the loads read the new key row as a stand-in, so they
     // stay unconditional; the values are then replaced by cos 1, sin 0.)
-    const float *cos_src = rope ? cos_row : reinterpret_cast<const float *>(p.new_key + new_base);
-    const float *sin_src = rope ? sin_row : reinterpret_cast<const float *>(p.new_key + new_base);
+    const float *stand_in = F32IO ? p.new_key32 + new_base : reinterpret_cast<const float *>(p.new_key + new_base);
+    const float *cos_src = rope ? cos_row : stand_in;
+    const float *sin_src = rope ? sin_row : stand_in;
     const float rc_raw = cos_src[lane];
     const float rs_raw = sin_src[lane];
     const float rc = rope ? rc_raw : 1.0f;
@@ -202,8 +239,8 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
                 const int pair = (kb & 1) * 32 + kg * 8 + j;
                 const float c = __shfl(rc, pair);
                 const float sn = __shfl(rs, pair);
-                const float x = static_cast<float>(qb[kb][j]);
-                const float y = static_cast<float>(qb[kb ^ 2][j]);
+                const float x = F32IO ? qf[kb][j] : static_cast<float>(qb[kb][j]);
+                const float y = F32IO ? qf[kb ^ 2][j] : static_cast<float>(qb[kb ^ 2][j]);
                 qr[kb][j] = kb < 2 ? to_h(x * c + (-y) * sn) : to_h(x * c + y * sn);
             }
         }
@@ -234,8 +271,8 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
         if (wave == (rel / kChunkTiles) % WAVES) {
             uint16_t k_lo = nk_lo, k_hi = nk_hi;
             if (rope) {
-                const float x = static_cast<float>(__builtin_bit_cast(_Float16, nk_lo));
-                const float y = static_cast<float>(__builtin_bit_cast(_Float16, nk_hi));
+                const float x = F32IO ? nkf_lo : static_cast<float>(__builtin_bit_cast(_Float16, nk_lo));
+                const float y = F32IO ? nkf_hi : static_cast<float>(__builtin_bit_cast(_Float16, nk_hi));
                 k_lo = __builtin_bit_cast(uint16_t, to_h(x * rc + (-y) * rs));
                 k_hi = __builtin_bit_cast(uint16_t, to_h(y * rc + x * rs));
             }
@@ -413,12 +450,17 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
         for (int e = 0; e < kPer; ++e) po[e] += sm_o[w][h][d0 + e] * f;
     }
 
-    uint16_t *out = p.out + (static_cast<size_t>(s) * kQueryHeads + g * kGroup) * kHeadDim;
+    // Output element i of this (sequence, kv head): fp16 (RNE) or f32.
+    const size_t out_off = (static_cast<size_t>(s) * kQueryHeads + g * kGroup) * kHeadDim;
+    auto put = [&](int i, float v) {
+        if constexpr (F32IO) p.out32[out_off + i] = v;
+        else p.out[out_off + i] = __builtin_bit_cast(uint16_t, to_h(v));
+    };
     if (num_parts == 1) {
         const float inv = 1.0f / L;
         if (active) {
 #pragma unroll
-            for (int e = 0; e < kPer; ++e) out[e0 + e] = __builtin_bit_cast(uint16_t, to_h(po[e] * inv));
+            for (int e = 0; e < kPer; ++e) put(e0 + e, po[e] * inv);
         }
         return;
     }
@@ -517,7 +559,7 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     const float inv = 1.0f / Lg;
     if (active) {
 #pragma unroll
-        for (int e = 0; e < kPer; ++e) out[e0 + e] = __builtin_bit_cast(uint16_t, to_h(og[e] * inv));
+        for (int e = 0; e < kPer; ++e) put(e0 + e, og[e] * inv);
     }
     if (threadIdx.x == 0)
         __hip_atomic_store(p.counters + s * kKvHeads + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -533,7 +575,7 @@ __device__ inline int64_t checked_cache_len(const DecodeParams &p, int64_t len) 
 
 // Grid (partition, kv head, sequence): sequences of one uniform length, or
 // ragged lengths when there are too many sequences for the ragged kernel.
-template <int WAVES, int PAIRS>
+template <int WAVES, int PAIRS, bool F32IO>
 __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParams p) {
     const uint32_t part = blockIdx.x;
     const uint32_t g = blockIdx.y;  // kv head
@@ -553,7 +595,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     const uint32_t ids =
         wave_tile_ids<WAVES, 2 * PAIRS>(p, s, part_start, min(part_start + P, cache_len + 1), wave, &bad);
     const int pos = p.positions ? load_const(p.positions, s) : cache_len;
-    decode_item<WAVES, PAIRS, false>(p, static_cast<int>(p.partition_tokens), s, g, part, cache_len, pos, ids, bad);
+    decode_item<WAVES, PAIRS, false, F32IO>(p, static_cast<int>(p.partition_tokens), s, g, part, cache_len, pos, ids,
+                                            bad);
 }
 
 // Exclusive scan of one int per thread over the workgroup; *total receives
@@ -587,7 +630,7 @@ __device__ inline int workgroup_exclusive_scan(int v, int *sm_wave_sums, int *to
 // blockIdx.x + gridDim.x, ...  Sequences with fewer partitions launch no
 // empty workgroups, so every compute unit stays on real work, and the block
 // ids of the next item are loaded while the current one runs.
-template <int WAVES, int PAIRS>
+template <int WAVES, int PAIRS, bool F32IO>
 __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(DecodeParams p, uint32_t num_seqs) {
     constexpr int kThreads = WAVES * 64;
     __shared__ int sm_first[kMaxRaggedSeqs + 1];  // first item (per kv head) of each sequence
@@ -695,7 +738,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
                                                    min(static_cast<int>(part_next + 1) * P, sm_len[s_next] + 1), wave,
                                                    &bad_next);
         }
-        decode_item<WAVES, PAIRS, true>(p, P, s, static_cast<uint32_t>(item & 1), part, sm_len[s], sm_pos[s], ids, bad);
+        decode_item<WAVES, PAIRS, true, F32IO>(p, P, s, static_cast<uint32_t>(item & 1), part, sm_len[s], sm_pos[s],
+                                               ids, bad);
         if (next >= items) break;
         __syncthreads();  // the next item reuses the workgroup's LDS
         item = next;
@@ -710,6 +754,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_ragged_kernel(Deco
 // (kv head, sequence); each thread folds 4 consecutive output elements of one
 // head over every partition, 16 partitions per batch of loads.  Sequences of
 // one partition were written directly by the ragged kernel.
+template <bool F32IO>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p) {
     const uint32_t g = blockIdx.x;
     const uint32_t s = blockIdx.y;
@@ -755,9 +800,12 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p)
         Mg = Mb;
     }
     const float inv = 1.0f / Lg;
-    uint16_t *out = p.out + (static_cast<size_t>(s) * kQueryHeads + g * kGroup) * kHeadDim + e0;
+    const size_t out_off = (static_cast<size_t>(s) * kQueryHeads + g * kGroup) * kHeadDim + e0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) out[e] = __builtin_bit_cast(uint16_t, to_h(og[e] * inv));
+    for (int e = 0; e < 4; ++e) {
+        if constexpr (F32IO) p.out32[out_off + e] = og[e] * inv;
+        else p.out[out_off + e] = __builtin_bit_cast(uint16_t, to_h(og[e] * inv));
+    }
 }
 
 __global__ void fill_u32_kernel(uint32_t *dst, size_t words, uint32_t value) {
@@ -815,6 +863,51 @@ uint32_t resident_workgroups(const void *kernel, int threads, uint64_t max_items
     return static_cast<uint32_t>(max_items < wgs ? (max_items ? max_items : 1) : wgs);
 }
 
+// One regime's launches for operands of either width (F32IO: the f32 entry
+// point's query, new key and value, output).
+template <bool F32IO>
+int launch_paged_decode_kernels(const DecodeLaunch &launch, DecodeParams &p, hipStream_t st) {
+    const pvlc_hip_paged_decode_args &a = *launch.args;
+    int e = 0;
+    if (launch.streaming) {
+        // Persistent kernel storing partials, then the merge kernel: no
+        // workgroup waits on a cross-workgroup hand-off.
+        const uint64_t max_items = static_cast<uint64_t>(launch.max_parts) * kKvHeads * a.num_seqs;
+#define PVLC_RAGGED_LAUNCH(W, PR)                                                                                  \
+    do {                                                                                                           \
+        const uint32_t wgs = resident_workgroups(                                                                  \
+            reinterpret_cast<const void *>(&paged_decode_ragged_kernel<W, PR, F32IO>), (W) * 64, max_items,        \
+            &p.compute_units, &e);                                                                                 \
+        if (e == 0) {                                                                                              \
+            hipLaunchKernelGGL((paged_decode_ragged_kernel<W, PR, F32IO>), dim3(wgs), dim3((W) * 64), 0, st, p,    \
+                               a.num_seqs);                                                                        \
+            hipLaunchKernelGGL(paged_decode_merge_kernel<F32IO>, dim3(kKvHeads, a.num_seqs), dim3(256), 0, st, p); \
+        }                                                                                                          \
+    } while (0)
+        if (launch.waves == 4) PVLC_RAGGED_LAUNCH(4, 1);
+        else PVLC_RAGGED_LAUNCH(2, 1);
+#undef PVLC_RAGGED_LAUNCH
+        if (e != 0) return e;
+        return static_cast<int>(hipGetLastError());
+    }
+
+    // Single-shot regime: one workgroup per (partition, kv head, sequence);
+    // the last partition to finish merges.
+    const dim3 grid(launch.max_parts, kKvHeads, a.num_seqs);
+#define PVLC_DECODE_LAUNCH(W, PR) \
+    hipLaunchKernelGGL((paged_decode_kernel<W, PR, F32IO>), grid, dim3((W) * 64), 0, st, p)
+    switch (launch.waves) {
+        case 2: PVLC_DECODE_LAUNCH(2, 1); break;
+        case 4: PVLC_DECODE_LAUNCH(4, 1); break;
+        case 6: PVLC_DECODE_LAUNCH(6, 1); break;
+        case 10: PVLC_DECODE_LAUNCH(10, 1); break;
+        case 12: PVLC_DECODE_LAUNCH(12, 1); break;
+        default: PVLC_DECODE_LAUNCH(8, 1); break;
+    }
+#undef PVLC_DECODE_LAUNCH
+    return static_cast<int>(hipGetLastError());
+}
+
 int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
     const pvlc_hip_paged_decode_args &a = *launch.args;
     DecodeParams p{};
@@ -843,43 +936,15 @@ int launch_paged_decode(const DecodeLaunch &launch, void *stream) {
     p.error_word = launch.error_word;
     p.partition_word = launch.partition_word;
     p.scale_log2 = kLog2e / sqrtf(static_cast<float>(kHeadDim));
-
     hipStream_t st = static_cast<hipStream_t>(stream);
-    int e = 0;
-    if (launch.streaming) {
-        // Persistent kernel storing partials, then the merge kernel: no
-        // workgroup waits on a cross-workgroup hand-off.
-        const uint64_t max_items = static_cast<uint64_t>(launch.max_parts) * kKvHeads * a.num_seqs;
-#define PVLC_RAGGED_LAUNCH(W, PR)                                                                                  \
-    do {                                                                                                           \
-        const uint32_t wgs = resident_workgroups(reinterpret_cast<const void *>(&paged_decode_ragged_kernel<W, PR>), \
-                                                 (W) * 64, max_items, &p.compute_units, &e);                       \
-        if (e == 0) {                                                                                              \
-            hipLaunchKernelGGL((paged_decode_ragged_kernel<W, PR>), dim3(wgs), dim3((W) * 64), 0, st, p, a.num_seqs); \
-            hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(kKvHeads, a.num_seqs), dim3(256), 0, st, p);       \
-        }                                                                                                          \
-    } while (0)
-        if (launch.waves == 4) PVLC_RAGGED_LAUNCH(4, 1);
-        else PVLC_RAGGED_LAUNCH(2, 1);
-#undef PVLC_RAGGED_LAUNCH
-        if (e != 0) return e;
-        return static_cast<int>(hipGetLastError());
+    if (launch.f32) {
+        p.query32 = launch.f32->query;
+        p.new_key32 = launch.f32->new_key;
+        p.new_value32 = launch.f32->new_value;
+        p.out32 = launch.f32->out;
+        return launch_paged_decode_kernels<true>(launch, p, st);
     }
-
-    // Single-shot regime: one workgroup per (partition, kv head, sequence);
-    // the last partition to finish merges.
-    const dim3 grid(launch.max_parts, kKvHeads, a.num_seqs);
-#define PVLC_DECODE_LAUNCH(W, PR) hipLaunchKernelGGL((paged_decode_kernel<W, PR>), grid, dim3((W) * 64), 0, st, p)
-    switch (launch.waves) {
-        case 2: PVLC_DECODE_LAUNCH(2, 1); break;
-        case 4: PVLC_DECODE_LAUNCH(4, 1); break;
-        case 6: PVLC_DECODE_LAUNCH(6, 1); break;
-        case 10: PVLC_DECODE_LAUNCH(10, 1); break;
-        case 12: PVLC_DECODE_LAUNCH(12, 1); break;
-        default: PVLC_DECODE_LAUNCH(8, 1); break;
-    }
-#undef PVLC_DECODE_LAUNCH
-    return static_cast<int>(hipGetLastError());
+    return launch_paged_decode_kernels<false>(launch, p, st);
 }
 
 int launch_fill_u32(uint32_t *dst, size_t words, uint32_t value, void *stream) {

@@ -114,6 +114,13 @@ size_t key_blocked_index(uint32_t token, uint32_t head, uint32_t dim);
 size_t value_blocked_index(uint32_t token, uint32_t head, uint32_t dim);
 
 // Kernel launchers (kernels_*.hip).  Return hipError_t as int.
+// The f32 operands of pvlc_hip_paged_decode_f32io (device pointers).
+struct DecodeOperands32 {
+    const float *query;      // [num_seqs][16][128]
+    const float *new_key;    // [num_seqs][2][128]
+    const float *new_value;  // [num_seqs][2][128]
+    float *out;              // [num_seqs][16][128]
+};
 struct DecodeLaunch {
     const pvlc_hip_paged_decode_args *args;
     uint32_t partition_tokens;
@@ -131,6 +138,9 @@ struct DecodeLaunch {
     // partition it used here for the merge kernel, and the compute units it
     // assumed in the next word (null: partition_tokens as is).
     uint32_t *partition_word;
+    // f32 operands instead of args' fp16 query, new key and value, output
+    // (null: the fp16 ones).
+    const DecodeOperands32 *f32 = nullptr;
 };
 int launch_paged_decode(const DecodeLaunch &launch, void *stream);
 int launch_fill_u32(uint32_t *dst, size_t words, uint32_t value, void *stream);
@@ -286,14 +296,17 @@ struct DecodeState {
     uint32_t part_stride;  // partials per (sequence, kv head) slot: max_parts rounded up to odd
 };
 // Checks of pvlc_hip_paged_decode_f16's arguments, the workspace aside: the
-// partition and the partitions per (sequence, kv head) of the launch.
+// partition and the partitions per (sequence, kv head) of the launch.  With
+// f32 operands (pvlc_hip_paged_decode_f32io) args' fp16 query, new key and
+// value and output must be NULL and the f32 ones given.
 pvlc_hip_status validate_decode_geometry(const pvlc_hip_paged_decode_args *a, uint32_t *partition_out,
-                                         uint32_t *max_parts_out);
+                                         uint32_t *max_parts_out, const DecodeOperands32 *f32 = nullptr);
 // Launch a validated decode with its split-K state at `state`; launches_out
 // receives the kernels launched (1, or 2 for the persistent kernel and its
 // merge kernel).
 pvlc_hip_status launch_decode_state(const pvlc_hip_paged_decode_args *a, uint32_t partition, uint32_t max_parts,
-                                    const DecodeState &state, void *stream, uint32_t *launches_out);
+                                    const DecodeState &state, void *stream, uint32_t *launches_out,
+                                    const DecodeOperands32 *f32 = nullptr);
 // Partition rules: balanced_parts is the partition count per (sequence, kv
 // head) of the single-shot rule; single_shot_partition returns 0 when a
 // partition would exceed kSingleShotTiles; auto_partition falls back to

@@ -174,11 +174,21 @@ namespace pvlc {
 // partitions per (sequence, kv head) the launch runs.  Returns a status
 // (0 = ok) without touching the GPU.
 pvlc_hip_status validate_decode_geometry(const pvlc_hip_paged_decode_args *a, uint32_t *partition_out,
-                                         uint32_t *max_parts_out) {
+                                         uint32_t *max_parts_out, const DecodeOperands32 *f32) {
     if (!a) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "paged decode args are NULL");
     if (a->num_seqs == 0 || a->num_blocks == 0 || a->max_blocks_per_seq == 0 || a->max_context == 0)
         return invalid(PVLC_HIP_INV_ZERO_DIMENSION, "all paged decode dimensions must be nonzero");
-    if (!a->key_cache || !a->value_cache || !a->query || !a->new_key || !a->new_value || !a->out)
+    if (f32) {
+        if (a->query || a->new_key || a->new_value || a->out)
+            return invalid(PVLC_HIP_INV_LENGTH_MISMATCH,
+                           "pvlc_hip_paged_decode_f32io takes its query, new key, new value and output as f32 "
+                           "arguments; the fp16 ones in the args must be NULL");
+        if (!f32->query || !f32->new_key || !f32->new_value || !f32->out)
+            return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "paged decode f32 operand pointer is NULL");
+    } else if (!a->query || !a->new_key || !a->new_value || !a->out) {
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "paged decode buffer pointer is NULL");
+    }
+    if (!a->key_cache || !a->value_cache)
         return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "paged decode buffer pointer is NULL");
     if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr) || (a->rope_cos && a->rope_rows == 0))
         return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION, "rotary tables must be given together with rows");
@@ -219,7 +229,8 @@ pvlc_hip_status validate_decode_geometry(const pvlc_hip_paged_decode_args *a, ui
 }
 
 pvlc_hip_status launch_decode_state(const pvlc_hip_paged_decode_args *a, uint32_t partition, uint32_t max_parts,
-                                    const DecodeState &state, void *stream, uint32_t *launches_out) {
+                                    const DecodeState &state, void *stream, uint32_t *launches_out,
+                                    const DecodeOperands32 *f32) {
     // Streaming regime: ragged lengths, or partitions longer than one chunk
     // of the largest single-shot workgroup.
     const uint32_t part_tiles = (partition + kBlockTokens - 1) / kBlockTokens;
@@ -236,7 +247,8 @@ pvlc_hip_status launch_decode_state(const pvlc_hip_paged_decode_args *a, uint32_
                         state.part_ml,
                         state.counters,
                         state.error_word,
-                        nullptr};
+                        nullptr,
+                        f32};
     // An automatic streaming launch records the partition it settled on and
     // the compute units it assumed in the two status words.
     if (streaming && a->partition_tokens == 0) launch.partition_word = state.status_words;
@@ -253,9 +265,9 @@ namespace {
 // The caller's workspace checked and laid out (decode_workspace_layout): the
 // error word first, the two status words after it in the same 256-byte slot.
 pvlc_hip_status launch_decode_checked(const pvlc_hip_paged_decode_args *a, void *stream,
-                                      uint32_t *launches_out = nullptr) {
+                                      uint32_t *launches_out = nullptr, const DecodeOperands32 *f32 = nullptr) {
     uint32_t partition = 0, max_parts = 0;
-    if (pvlc_hip_status st = validate_decode_geometry(a, &partition, &max_parts)) return st;
+    if (pvlc_hip_status st = validate_decode_geometry(a, &partition, &max_parts, f32)) return st;
     if (!a->workspace) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "paged decode workspace is NULL");
     const DecodeWorkspace layout = decode_workspace_layout(a->num_seqs, max_parts);
     if (a->workspace_bytes < layout.total)
@@ -268,7 +280,7 @@ pvlc_hip_status launch_decode_checked(const pvlc_hip_paged_decode_args *a, void 
                             reinterpret_cast<uint32_t *>(ws + layout.error_offset),
                             reinterpret_cast<uint32_t *>(ws + layout.error_offset) + 1,
                             layout.part_stride};
-    return launch_decode_state(a, partition, max_parts, state, stream, launches_out);
+    return launch_decode_state(a, partition, max_parts, state, stream, launches_out, f32);
 }
 
 // Session creation shared by begin_decoder_kv_session and the one-shot path.
@@ -776,6 +788,13 @@ pvlc_hip_status pvlc_hip_workspace_error(const void *workspace, size_t workspace
 
 pvlc_hip_status pvlc_hip_paged_decode_f16(const pvlc_hip_paged_decode_args *args, void *stream) {
     if (pvlc_hip_status st = launch_decode_checked(args, stream)) return st;
+    return ok();
+}
+
+pvlc_hip_status pvlc_hip_paged_decode_f32io(const pvlc_hip_paged_decode_args *args, const float *query,
+                                            const float *new_key, const float *new_value, float *out, void *stream) {
+    const DecodeOperands32 f32{query, new_key, new_value, out};
+    if (pvlc_hip_status st = launch_decode_checked(args, stream, nullptr, &f32)) return st;
     return ok();
 }
 

@@ -1,11 +1,14 @@
 """The decoder token step on this backend's entry points (bench.TokenChain): per layer a grouped q|k|v GEMV, the
 single-layer paged decode (rotary on q and the new key, append, GQA), the o GEMV, a grouped gate|up GEMV and the
 down GEMV, then the LM head fused with the greedy top-1 -- the per-layer chain the reference's stack session
-issues (crates/pvlc-runtime-web/src/web/decoder_stack_session.rs:4625-4797).  Checks, at 3 layers and T=300:
+issues (crates/pvlc-runtime-web/src/web/decoder_stack_session.rs:4625-4797).  The decode runs on the f32 operands
+the projections write (pvlc_hip_paged_decode_f32io), or through fp16 conversions and the fp16 entry point.
+Checks, at 3 layers and T=300:
 
 - every layer's attention against decode_gqa_f32 (cpu-ref lib.rs:858-927) over that layer's cached rows plus
-  the appended row, on the q|k|v the chain computed (q rotated with apply_rope_neox, the key rotated and rounded
-  to fp16), within max-abs 2e-3 and relative L2 1e-2; every layer's cache rows bit-exact after the append;
+  the appended row, on the q|k|v the chain computed (q rotated with apply_rope_neox and rounded to fp16 -- from
+  its f32 value with f32 operands --, the key likewise), within max-abs 2e-3 and relative L2 1e-2; every layer's
+  cache rows bit-exact after the append;
 - the top-1 result names a maximal logit and carries its bits;
 - replays of the step captured in a HIP graph, with eager work and synchronisations between them, equal the
   eager step bit for bit in every buffer the step writes.
@@ -21,11 +24,13 @@ from pvlc_testlib import W, check_close, from_dev, log, pvlc, rope_k_f16, widen
 pytestmark = pytest.mark.gpu
 
 
-def test_token_chain_against_the_oracle_and_replayed_from_a_graph():
+@pytest.mark.parametrize("f32_operands", [True, False])
+def test_token_chain_against_the_oracle_and_replayed_from_a_graph(f32_operands):
     import torch
     layers, context, capacity = 3, 300, 320
-    log(f"case: decoder token chain, {layers} layers, T={context}")
-    chain = bench.TokenChain(pvlc, torch, layers, context, capacity, head_rows=20_000, seed=5)
+    log(f"case: decoder token chain, {layers} layers, T={context}, f32 operands {f32_operands}")
+    chain = bench.TokenChain(pvlc, torch, layers, context, capacity, head_rows=20_000, seed=5,
+                             f32_operands=f32_operands)
     stream = torch.cuda.current_stream()
     before = []
     for l in range(layers):
@@ -38,13 +43,22 @@ def test_token_chain_against_the_oracle_and_replayed_from_a_graph():
     torch.cuda.synchronize()
     pos = context - 1
     for l in range(layers):
-        qkv = from_dev(chain.qkv16[l].view(torch.int16))
-        q = O.rope_neox_f32(widen(qkv[:2048]), 16, 128, 128, [pos] * 16, 500000.0)
-        k_new = rope_k_f16(qkv[2048:2304], pos)
+        if f32_operands:
+            qkv = chain.qkv32[l].cpu().numpy()
+            q = widen(O.f32_to_f16(O.rope_neox_f32(qkv[:2048], 16, 128, 128, [pos] * 16, 500000.0)))
+            k_new = O.f32_to_f16(O.rope_neox_f32(qkv[2048:2304], 2, 128, 128, [pos] * 2, 500000.0))
+            v_new = O.f32_to_f16(qkv[2304:2560])
+            got = chain.attn32[l].cpu().numpy()
+        else:
+            qkv = from_dev(chain.qkv16[l].view(torch.int16))
+            q = O.rope_neox_f32(widen(qkv[:2048]), 16, 128, 128, [pos] * 16, 500000.0)
+            k_new = rope_k_f16(qkv[2048:2304], pos)
+            v_new = qkv[2304:2560]
+            got = widen(from_dev(chain.attn16[l].view(torch.int16)))
         keys = np.concatenate([before[l][0], k_new])
-        values = np.concatenate([before[l][1], qkv[2304:2560]])
+        values = np.concatenate([before[l][1], v_new])
         want = O.decode_gqa_f32(q, widen(keys), widen(values), context, 16, 2, 128)
-        check_close(widen(from_dev(chain.attn16[l].view(torch.int16))), want, f"chain layer {l}")
+        check_close(got, want, f"chain layer {l}")
         kr = torch.empty(context * W, dtype=torch.float16, device="cuda")
         vr = torch.empty_like(kr)
         off = l * chain.nb * 16 * W
@@ -59,7 +73,7 @@ def test_token_chain_against_the_oracle_and_replayed_from_a_graph():
     eager = chain.state()
     graph = chain.capture(chain.step)
     for rep in range(3):
-        for t in chain.attn16 + chain.qkv16:
+        for t in chain.attn16 + chain.qkv16 + chain.attn32 + chain.qkv32:
             t.zero_()  # eager work between replays
         chain.result.zero_()
         graph.replay()

@@ -301,3 +301,26 @@ def test_prefill_rejects_a_short_or_misaligned_workspace():
     with pytest.raises(pvlc.PvlcHipError) as e:
         pvlc.paged_prefill_f16(**common, workspace=fake + 4, workspace_bytes=need)
     assert e.value.invocation_code == "LengthMismatch"
+
+
+def test_f32_operand_decode_rejects_mixed_or_missing_operands():
+    """pvlc_hip_paged_decode_f32io takes the query, new key and value and output as f32 arguments: fp16 ones left
+    in the args, or a missing f32 one, are rejected before any GPU effect (placeholder addresses, never read)."""
+    fake = 1 << 20
+    common = dict(num_seqs=1, num_blocks=1, max_blocks_per_seq=1, key_cache=fake, value_cache=fake, workspace=fake,
+                  workspace_bytes=1 << 20, max_context=16, uniform_cache_len=0)
+    mixed = pvlc.paged_decode_args(query=fake, new_key=None, new_value=None, out=None, **common)
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.paged_decode_f32io(mixed, fake, fake, fake, fake)
+    assert code(e) == ("InvalidInvocation", "LengthMismatch") and "must be NULL" in str(e.value)
+    bare = pvlc.paged_decode_args(query=None, new_key=None, new_value=None, out=None, **common)
+    for missing in range(4):
+        ptrs = [fake] * 4
+        ptrs[missing] = None
+        with pytest.raises(pvlc.PvlcHipError) as e:
+            pvlc.paged_decode_f32io(bare, *ptrs)
+        assert code(e) == ("InvalidInvocation", "LengthMismatch") and "f32 operand pointer is NULL" in str(e.value)
+    # and the fp16 entry point still requires its own operands
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.paged_decode_f16(bare)
+    assert code(e) == ("InvalidInvocation", "LengthMismatch")
