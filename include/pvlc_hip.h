@@ -469,6 +469,19 @@ size_t pvlc_hip_paged_prefill_workspace_bytes(uint32_t tokens);
  * decoder_prefill_gqa_f32 (pvlc-wgsl lib.rs:1262-1416; issued by
  * decoder_stack_session.rs:5044-5064). */
 pvlc_hip_status pvlc_hip_paged_prefill_f16(const pvlc_hip_paged_prefill_args *args, void *stream);
+/* The same prefill with the per-token operands in f32, as the reference's
+ * prefill chain passes them (decoder_prefill_mrope_f32 reads the projections'
+ * f32 q/k/v, decoder_prefill_gqa_f32 writes the f32 output the o projection
+ * reads; pvlc-wgsl lib.rs:1262-1416, web decoder_stack_session.rs:5044-5064):
+ * query [tokens][16][128], key and value [tokens][2][128], out
+ * [tokens][16][128], all f32 device pointers.  The query and the keys are
+ * rotated from their f32 values and rounded to fp16 once (RNE), the values
+ * rounded to fp16; the cache (and the optional query scratch) stays fp16; the
+ * output is the normalised f32 product o * (1/l), which the fp16 entry point
+ * rounds to fp16 once from the exact product.  args->query, key, value and out
+ * must be NULL; everything else as pvlc_hip_paged_prefill_f16. */
+pvlc_hip_status pvlc_hip_paged_prefill_f32io(const pvlc_hip_paged_prefill_args *args, const float *query,
+                                             const float *key, const float *value, float *out, void *stream);
 
 /* Compact [tokens][2][128] fp16 rows <-> blocked planes (bit-exact), rows
  * 0..tokens-1 of one sequence through its block table (NULL = blocks 0..). */

@@ -210,6 +210,7 @@ SIGNATURES = {
     "pvlc_hip_paged_decode_f16_no_alloc": ([ctypes.POINTER(PagedDecodeArgsC), _VP, _VP], ctypes.c_int32),
     "pvlc_hip_paged_decode_f32io": ([ctypes.POINTER(PagedDecodeArgsC), _VP, _VP, _VP, _VP, _VP], ctypes.c_int32),
     "pvlc_hip_paged_prefill_f16": ([ctypes.POINTER(PagedPrefillArgsC), _VP], ctypes.c_int32),
+    "pvlc_hip_paged_prefill_f32io": ([ctypes.POINTER(PagedPrefillArgsC), _VP, _VP, _VP, _VP, _VP], ctypes.c_int32),
     "pvlc_hip_kv_pack_f16": ([_VP, _VP, _U32, _VP, _U32, _VP, _VP, _VP], ctypes.c_int32),
     "pvlc_hip_kv_unpack_f16": ([_VP, _VP, _U32, _VP, _U32, _VP, _VP, _VP], ctypes.c_int32),
     "pvlc_hip_gemv_tiled_plan_create": ([_U32, _U32, ctypes.POINTER(GemvTiledPlanC)], ctypes.c_int32),
@@ -753,6 +754,17 @@ def paged_prefill_f16(*, tokens, num_blocks, key_cache, value_cache, query, key,
                           _ptr(key), _ptr(value), _ptr(out), _ptr(rope_cos), _ptr(rope_sin), rope_rows,
                           _ptr(positions), _ptr(query_scratch), _ptr(error_word), _ptr(workspace), workspace_bytes)
     _check(lib.pvlc_hip_paged_prefill_f16(ctypes.byref(a), _stream(stream)))
+
+
+def paged_prefill_f32io(*, tokens, num_blocks, key_cache, value_cache, query, key, value, out, query_scratch=None,
+                        block_table=None, rope_cos=None, rope_sin=None, rope_rows=0, positions=None,
+                        error_word=None, workspace=None, workspace_bytes=0, stream=None) -> None:
+    """paged_prefill_f16 with f32 query, key, value and output, the reference chain's operand format."""
+    a = PagedPrefillArgsC(tokens, num_blocks, _ptr(block_table), _ptr(key_cache), _ptr(value_cache), None, None,
+                          None, None, _ptr(rope_cos), _ptr(rope_sin), rope_rows, _ptr(positions),
+                          _ptr(query_scratch), _ptr(error_word), _ptr(workspace), workspace_bytes)
+    _check(lib.pvlc_hip_paged_prefill_f32io(ctypes.byref(a), _ptr(query), _ptr(key), _ptr(value), _ptr(out),
+                                            _stream(stream)))
 
 
 def kv_pack_f16(key_rows, value_rows, tokens, key_cache, value_cache, num_blocks, block_table=None,

@@ -65,6 +65,12 @@ struct PrefillParams {
     bool split;
     uint32_t *counters;  // [pair][kv head]
     float *partials;     // [pair][kv head][2 parts][kPrefillPartialFloats]
+    // f32 operands (pvlc_hip_paged_prefill_f32io): query, key, value, output;
+    // null for the fp16 entry point.
+    const float *query32;
+    const float *key32;
+    const float *value32;
+    float *out32;
 };
 
 __device__ inline uint32_t cache_block(const PrefillParams &p, uint32_t tile, bool *ok) {
@@ -96,6 +102,7 @@ __device__ inline int rope_position(const PrefillParams &p, uint32_t t, bool *ro
     return pos;
 }
 
+template <bool F32IO>
 __global__ __launch_bounds__(kAppendThreads) void prefill_rope_append_kernel(PrefillParams p) {
     const int i = threadIdx.x;
     const uint32_t b = blockIdx.x;  // cache block (16 tokens) of the sequence
@@ -110,7 +117,10 @@ __global__ __launch_bounds__(kAppendThreads) void prefill_rope_append_kernel(Pre
     for (int r = 0; r < 2; ++r) {
         const int k = i + r * kAppendThreads;
         const uint32_t t = t0 + min(static_cast<uint32_t>(k >> 5), ntok - 1);
-        vrow[r] = *reinterpret_cast<const u16x8_t *>(p.value + static_cast<size_t>(t) * kRowElems + (k & 31) * 8);
+        if constexpr (F32IO)
+            vrow[r] = __builtin_bit_cast(u16x8_t, round_chunk(p.value32 + static_cast<size_t>(t) * kRowElems + (k & 31) * 8));
+        else
+            vrow[r] = *reinterpret_cast<const u16x8_t *>(p.value + static_cast<size_t>(t) * kRowElems + (k & 31) * 8);
     }
 
     bool ok;
@@ -126,10 +136,18 @@ __global__ __launch_bounds__(kAppendThreads) void prefill_rope_append_kernel(Pre
             bool rope;
             const int pos = rope_position(p, t, &rope);
             if (!rope && p.rope_cos != nullptr && c == 0 && hh == 0 && p.error_word) atomicOr(p.error_word, 4u);
-            const uint16_t *krow = p.key + (static_cast<size_t>(t) * kKvHeads + hh) * kHeadDim;
-            const half8_t kv = rope ? rotate_chunk(krow, c * 8, p.rope_cos + static_cast<size_t>(pos) * 64,
-                                                   p.rope_sin + static_cast<size_t>(pos) * 64)
-                                    : *reinterpret_cast<const half8_t *>(krow + c * 8);
+            const size_t koff = (static_cast<size_t>(t) * kKvHeads + hh) * kHeadDim;
+            half8_t kv;
+            if constexpr (F32IO) {
+                kv = rope ? rotate_chunk(p.key32 + koff, c * 8, p.rope_cos + static_cast<size_t>(pos) * 64,
+                                         p.rope_sin + static_cast<size_t>(pos) * 64)
+                          : round_chunk(p.key32 + koff + c * 8);
+            } else {
+                const uint16_t *krow = p.key + koff;
+                kv = rope ? rotate_chunk(krow, c * 8, p.rope_cos + static_cast<size_t>(pos) * 64,
+                                         p.rope_sin + static_cast<size_t>(pos) * 64)
+                          : *reinterpret_cast<const half8_t *>(krow + c * 8);
+            }
             const size_t slab = (static_cast<size_t>(blk) * kKvHeads + hh) * kBlockHeadElems;
             if (ok) *reinterpret_cast<half8_t *>(p.key_cache + slab + c * 128 + key_slot(tt) * 8) = kv;
         }
@@ -168,10 +186,18 @@ __global__ __launch_bounds__(kAppendThreads) void prefill_rope_append_kernel(Pre
             const int h = (k >> 4) % kQueryHeads, d0 = (k & 15) * 8;
             bool rope;
             const int pos = rope_position(p, tq, &rope);
-            const uint16_t *qrow = p.query + (static_cast<size_t>(tq) * kQueryHeads + h) * kHeadDim;
-            const half8_t q = rope ? rotate_chunk(qrow, d0, p.rope_cos + static_cast<size_t>(pos) * 64,
-                                                  p.rope_sin + static_cast<size_t>(pos) * 64)
-                                   : *reinterpret_cast<const half8_t *>(qrow + d0);
+            const size_t qoff = (static_cast<size_t>(tq) * kQueryHeads + h) * kHeadDim;
+            half8_t q;
+            if constexpr (F32IO) {
+                q = rope ? rotate_chunk(p.query32 + qoff, d0, p.rope_cos + static_cast<size_t>(pos) * 64,
+                                        p.rope_sin + static_cast<size_t>(pos) * 64)
+                         : round_chunk(p.query32 + qoff + d0);
+            } else {
+                const uint16_t *qrow = p.query + qoff;
+                q = rope ? rotate_chunk(qrow, d0, p.rope_cos + static_cast<size_t>(pos) * 64,
+                                        p.rope_sin + static_cast<size_t>(pos) * 64)
+                         : *reinterpret_cast<const half8_t *>(qrow + d0);
+            }
             *reinterpret_cast<half8_t *>(p.qrot + (static_cast<size_t>(tq) * kQueryHeads + h) * kHeadDim + d0) = q;
         }
     }
@@ -204,6 +230,7 @@ __device__ inline void prefill_item(int b, int qblocks, int *qb, uint32_t *g) {
     }
 }
 
+template <bool F32IO>
 __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(PrefillParams p) {
     const int n = static_cast<int>(p.tokens);
     const int qblocks = (n + kQueryBlock - 1) / kQueryBlock;
@@ -258,24 +285,57 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
         const int h = static_cast<int>(g) * kGroup + wave * 2 + ct;
-        const uint16_t *qrow = p.query + (static_cast<size_t>(tq) * kQueryHeads + h) * kHeadDim;
-        half8_t raw[4];
+        const size_t qoff = (static_cast<size_t>(tq) * kQueryHeads + h) * kHeadDim;
+        if constexpr (F32IO) {
+            // f32 query: rotated from its f32 values and rounded once.
+            float raw[4][8];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) raw[kb] = *reinterpret_cast<const half8_t *>(qrow + kb * 32 + kg * 8);
+            for (int kb = 0; kb < 4; ++kb) {
+                const float4_t lo = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8);
+                const float4_t hi = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8 + 4);
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            half8_t q = raw[kb];
-            if (qrope) {
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const float c = qc[kb & 1][jj >> 2][jj & 3];
-                    const float sn = qs[kb & 1][jj >> 2][jj & 3];
-                    const float x = static_cast<float>(raw[kb][jj]);
-                    const float y = static_cast<float>(raw[kb ^ 2][jj]);
-                    q[jj] = kb < 2 ? to_h(x * c + (-y) * sn) : to_h(x * c + y * sn);
+                for (int jj = 0; jj < 4; ++jj) {
+                    raw[kb][jj] = lo[jj];
+                    raw[kb][jj + 4] = hi[jj];
                 }
             }
-            qf[ct][kb] = my_token < n ? q : half8_t{};
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                half8_t q;
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    if (qrope) {
+                        const float c = qc[kb & 1][jj >> 2][jj & 3];
+                        const float sn = qs[kb & 1][jj >> 2][jj & 3];
+                        const float x = raw[kb][jj];
+                        const float y = raw[kb ^ 2][jj];
+                        q[jj] = kb < 2 ? to_h(x * c + (-y) * sn) : to_h(x * c + y * sn);
+                    } else {
+                        q[jj] = to_h(raw[kb][jj]);
+                    }
+                }
+                qf[ct][kb] = my_token < n ? q : half8_t{};
+            }
+        } else {
+            const uint16_t *qrow = p.query + qoff;
+            half8_t raw[4];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) raw[kb] = *reinterpret_cast<const half8_t *>(qrow + kb * 32 + kg * 8);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                half8_t q = raw[kb];
+                if (qrope) {
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const float c = qc[kb & 1][jj >> 2][jj & 3];
+                        const float sn = qs[kb & 1][jj >> 2][jj & 3];
+                        const float x = static_cast<float>(raw[kb][jj]);
+                        const float y = static_cast<float>(raw[kb ^ 2][jj]);
+                        q[jj] = kb < 2 ? to_h(x * c + (-y) * sn) : to_h(x * c + y * sn);
+                    }
+                }
+                qf[ct][kb] = my_token < n ? q : half8_t{};
+            }
         }
     }
 
@@ -610,9 +670,12 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
             const float inv = 1.0f / o[ct][8][r];
             const int t = t0 + kg_e * 4 + r;
             if (t < n) {
-                uint16_t *orow = p.out + (static_cast<size_t>(t) * kQueryHeads + h) * kHeadDim;
+                const size_t ooff = (static_cast<size_t>(t) * kQueryHeads + h) * kHeadDim;
 #pragma unroll
-                for (int c = 0; c < 8; ++c) orow[c * 16 + row_e] = __builtin_bit_cast(uint16_t, to_h(o[ct][c][r] * inv));
+                for (int c = 0; c < 8; ++c) {
+                    if constexpr (F32IO) p.out32[ooff + c * 16 + row_e] = o[ct][c][r] * inv;
+                    else p.out[ooff + c * 16 + row_e] = __builtin_bit_cast(uint16_t, to_h(o[ct][c][r] * inv));
+                }
             }
         }
     }
@@ -625,7 +688,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
 
 }  // namespace
 
-int launch_prefill(const pvlc_hip_paged_prefill_args *a, void *stream) {
+int launch_prefill(const pvlc_hip_paged_prefill_args *a, void *stream, const PrefillOperands32 *f32) {
     PrefillParams p{};
     p.tokens = a->tokens;
     p.num_blocks = a->num_blocks;
@@ -643,9 +706,16 @@ int launch_prefill(const pvlc_hip_paged_prefill_args *a, void *stream) {
     p.qrot = a->query_scratch;
     p.error_word = a->error_word;
     p.scale_log2 = kLog2e / sqrtf(static_cast<float>(kHeadDim));
+    if (f32) {
+        p.query32 = f32->query;
+        p.key32 = f32->key;
+        p.value32 = f32->value;
+        p.out32 = f32->out;
+    }
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(prefill_rope_append_kernel, dim3((a->tokens + kBlockTokens - 1) / kBlockTokens),
-                       dim3(kAppendThreads), 0, st, p);
+    const dim3 append_grid((a->tokens + kBlockTokens - 1) / kBlockTokens);
+    if (f32) hipLaunchKernelGGL(prefill_rope_append_kernel<true>, append_grid, dim3(kAppendThreads), 0, st, p);
+    else hipLaunchKernelGGL(prefill_rope_append_kernel<false>, append_grid, dim3(kAppendThreads), 0, st, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     const unsigned qblocks = (a->tokens + kQueryBlock - 1) / kQueryBlock;
@@ -656,7 +726,8 @@ int launch_prefill(const pvlc_hip_paged_prefill_args *a, void *stream) {
         p.partials = reinterpret_cast<float *>(static_cast<unsigned char *>(a->workspace) + ws.partial_offset);
     }
     const unsigned grid = p.split ? prefill_pair_workgroups(qblocks) : qblocks * kKvHeads;
-    hipLaunchKernelGGL(prefill_attention_kernel, dim3(grid), dim3(kWaves * 64), 0, st, p);
+    if (f32) hipLaunchKernelGGL(prefill_attention_kernel<true>, dim3(grid), dim3(kWaves * 64), 0, st, p);
+    else hipLaunchKernelGGL(prefill_attention_kernel<false>, dim3(grid), dim3(kWaves * 64), 0, st, p);
     return static_cast<int>(hipGetLastError());
 }
 

@@ -51,4 +51,42 @@ __device__ inline half8_t rotate_chunk(const uint16_t *row, int d0, const float 
     return r;
 }
 
+// The same rotation of an f32 row (the f32-operand entry points): the same
+// products and sum from the f32 values, one RNE rounding to fp16.
+__device__ inline half8_t rotate_chunk(const float *row, int d0, const float *cos_row, const float *sin_row) {
+    const int dp = d0 < 64 ? d0 + 64 : d0 - 64;
+    const float4_t x0 = *reinterpret_cast<const float4_t *>(row + d0);
+    const float4_t x1 = *reinterpret_cast<const float4_t *>(row + d0 + 4);
+    const float4_t y0 = *reinterpret_cast<const float4_t *>(row + dp);
+    const float4_t y1 = *reinterpret_cast<const float4_t *>(row + dp + 4);
+    const float4_t c0 = *reinterpret_cast<const float4_t *>(cos_row + (d0 & 63));
+    const float4_t c1 = *reinterpret_cast<const float4_t *>(cos_row + (d0 & 63) + 4);
+    const float4_t s0 = *reinterpret_cast<const float4_t *>(sin_row + (d0 & 63));
+    const float4_t s1 = *reinterpret_cast<const float4_t *>(sin_row + (d0 & 63) + 4);
+    const float sign = d0 < 64 ? -1.0f : 1.0f;
+    half8_t r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float c = j < 4 ? c0[j] : c1[j - 4];
+        const float s = j < 4 ? s0[j] : s1[j - 4];
+        const float xc = (j < 4 ? x0[j] : x1[j - 4]) * c;
+        const float ps = (sign * (j < 4 ? y0[j] : y1[j - 4])) * s;
+        r[j] = to_h(xc + ps);
+    }
+    return r;
+}
+
+// 8 consecutive f32 values rounded (RNE) to fp16.
+__device__ inline half8_t round_chunk(const float *src) {
+    const float4_t a = *reinterpret_cast<const float4_t *>(src);
+    const float4_t b = *reinterpret_cast<const float4_t *>(src + 4);
+    half8_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        r[j] = to_h(a[j]);
+        r[j + 4] = to_h(b[j]);
+    }
+    return r;
+}
+
 }  // namespace pvlc

@@ -149,7 +149,14 @@ int launch_kv_pack(const uint16_t *key_rows, const uint16_t *value_rows, uint32_
                    void *stream);
 int launch_kv_unpack(const uint16_t *key_cache, const uint16_t *value_cache, uint32_t tokens, const int32_t *table,
                      uint32_t num_blocks, uint16_t *key_rows, uint16_t *value_rows, void *stream);
-int launch_prefill(const pvlc_hip_paged_prefill_args *args, void *stream);
+// The f32 operands of pvlc_hip_paged_prefill_f32io (device pointers).
+struct PrefillOperands32 {
+    const float *query;  // [tokens][16][128]
+    const float *key;    // [tokens][2][128]
+    const float *value;  // [tokens][2][128]
+    float *out;          // [tokens][16][128]
+};
+int launch_prefill(const pvlc_hip_paged_prefill_args *args, void *stream, const PrefillOperands32 *f32 = nullptr);
 
 // Prefill projection with fp16 weights: workspace of the exact hi/lo split
 // of the activations ([rows][K] fp16 each) and the per-row exponents.

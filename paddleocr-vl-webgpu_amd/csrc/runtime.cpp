@@ -828,11 +828,24 @@ pvlc_hip_status pvlc_hip_kv_unpack_f16(const uint16_t *key_cache, const uint16_t
 
 size_t pvlc_hip_paged_prefill_workspace_bytes(uint32_t tokens) { return prefill_workspace_layout(tokens).total; }
 
-pvlc_hip_status pvlc_hip_paged_prefill_f16(const pvlc_hip_paged_prefill_args *args, void *stream) {
+namespace {
+
+// Checks and launch shared by the fp16 and f32-operand prefill entry points.
+pvlc_hip_status prefill_checked(const pvlc_hip_paged_prefill_args *args, void *stream, const PrefillOperands32 *f32) {
     if (!args) return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill args are NULL");
     if (args->tokens == 0 || args->num_blocks == 0)
         return invalid(PVLC_HIP_INV_ZERO_DIMENSION, "tokens and blocks must be nonzero");
-    if (!args->query || !args->key || !args->value || !args->out || !args->key_cache || !args->value_cache)
+    if (f32) {
+        if (args->query || args->key || args->value || args->out)
+            return invalid(PVLC_HIP_INV_LENGTH_MISMATCH,
+                           "pvlc_hip_paged_prefill_f32io takes its query, key, value and output as f32 arguments; "
+                           "the fp16 ones in the args must be NULL");
+        if (!f32->query || !f32->key || !f32->value || !f32->out)
+            return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill f32 operand pointer is NULL");
+    } else if (!args->query || !args->key || !args->value || !args->out) {
+        return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill buffer pointer is NULL");
+    }
+    if (!args->key_cache || !args->value_cache)
         return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill buffer pointer is NULL");
     if ((args->rope_cos == nullptr) != (args->rope_sin == nullptr) || (args->rope_cos && args->rope_rows == 0))
         return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION, "rotary tables must be given together with rows");
@@ -850,9 +863,21 @@ pvlc_hip_status pvlc_hip_paged_prefill_f16(const pvlc_hip_paged_prefill_args *ar
         if (reinterpret_cast<uintptr_t>(args->workspace) % 256 != 0)
             return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill workspace must be 256-byte aligned");
     }
-    const int e = launch_prefill(args, stream);
+    const int e = launch_prefill(args, stream, f32);
     if (e != 0) return hip_fail(static_cast<hipError_t>(e), "prefill launch");
     return ok();
+}
+
+}  // namespace
+
+pvlc_hip_status pvlc_hip_paged_prefill_f16(const pvlc_hip_paged_prefill_args *args, void *stream) {
+    return prefill_checked(args, stream, nullptr);
+}
+
+pvlc_hip_status pvlc_hip_paged_prefill_f32io(const pvlc_hip_paged_prefill_args *args, const float *query,
+                                             const float *key, const float *value, float *out, void *stream) {
+    const PrefillOperands32 f32{query, key, value, out};
+    return prefill_checked(args, stream, &f32);
 }
 
 }  // extern "C"

@@ -324,3 +324,26 @@ def test_f32_operand_decode_rejects_mixed_or_missing_operands():
     with pytest.raises(pvlc.PvlcHipError) as e:
         pvlc.paged_decode_f16(bare)
     assert code(e) == ("InvalidInvocation", "LengthMismatch")
+
+
+def test_f32_operand_prefill_rejects_mixed_or_missing_operands():
+    """pvlc_hip_paged_prefill_f32io takes the query, key, value and output as f32 arguments: fp16 ones left in the
+    args, or a missing f32 one, are rejected before any GPU effect (placeholder addresses, never read)."""
+    fake = 1 << 20
+    mixed = pvlc.PagedPrefillArgsC(16, 1, None, fake, fake, fake, None, None, None, None, None, 0, None, None, None,
+                                   None, 0)
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc._check(pvlc.lib.pvlc_hip_paged_prefill_f32io(ctypes.byref(mixed), fake, fake, fake, fake, None))
+    assert code(e) == ("InvalidInvocation", "LengthMismatch") and "must be NULL" in str(e.value)
+    for missing in range(4):
+        ptrs = [fake] * 4
+        ptrs[missing] = None
+        with pytest.raises(pvlc.PvlcHipError) as e:
+            pvlc.paged_prefill_f32io(tokens=16, num_blocks=1, key_cache=fake, value_cache=fake, query=ptrs[0],
+                                     key=ptrs[1], value=ptrs[2], out=ptrs[3])
+        assert code(e) == ("InvalidInvocation", "LengthMismatch") and "f32 operand pointer is NULL" in str(e.value)
+    # and the fp16 entry point still requires its own operands
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.paged_prefill_f16(tokens=16, num_blocks=1, key_cache=fake, value_cache=fake, query=None, key=None,
+                               value=None, out=None)
+    assert code(e) == ("InvalidInvocation", "LengthMismatch")
