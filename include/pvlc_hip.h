@@ -465,6 +465,8 @@ size_t pvlc_hip_paged_prefill_workspace_bytes(uint32_t tokens);
 
 /* Causal prefill: rotary on Q and K, write all N K/V rows into the blocked
  * cache, then MFMA causal GQA attention (fp16 in, f32 accumulate, fp16 out).
+ * Query, key, value, output, caches and query scratch are 16-byte aligned
+ * (rejected otherwise).
  * Replaces decoder_prefill_mrope_f32 -> decoder_kv_append_range_f32 ->
  * decoder_prefill_gqa_f32 (pvlc-wgsl lib.rs:1262-1416; issued by
  * decoder_stack_session.rs:5044-5064). */

@@ -251,8 +251,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     // them at compile time, so the compiler sees that a step's loads into LDS
     // and its LDS reads touch different buffers and does not wait for the
     // loads before the reads.
-    __shared__ uint16_t sk0[kStepElems], sk1[kStepElems];
-    __shared__ uint16_t sv0[kStepElems], sv1[kStepElems];
+    __shared__ __align__(16) uint16_t sk0[kStepElems], sk1[kStepElems];
+    __shared__ __align__(16) uint16_t sv0[kStepElems], sv1[kStepElems];
     __shared__ bool sm_last;
 
   // One segment: a whole query block, or one part of a split one.
@@ -661,24 +661,45 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     }
 
     // Normalise: output row kg*4 + r of tile ct is query token t0 + kg*4 + r;
-    // its row sum is element r of the sums tile in the same lane.
+    // its row sum is element r of the sums tile in the same lane.  Each wave
+    // stages its two heads' 16 x 128 outputs in its own K/V buffer (free after
+    // the last step: no load into LDS is in flight) as [head][token][dim],
+    // then stores whole 16-byte chunks (8 fp16 or 4 f32 outputs) instead of
+    // one 2- or 4-byte element per lane and store.
+    using OutT = std::conditional_t<F32IO, float, uint16_t>;
+    constexpr int kChunk = 16 / static_cast<int>(sizeof(OutT));  // outputs per 16-byte chunk
+    OutT *stage = reinterpret_cast<OutT *>(wave == 0 ? sk0 : wave == 1 ? sk1 : wave == 2 ? sv0 : sv1);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-        const int h = static_cast<int>(g) * kGroup + wave * 2 + ct;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const float inv = 1.0f / o[ct][8][r];
-            const int t = t0 + kg_e * 4 + r;
-            if (t < n) {
-                const size_t ooff = (static_cast<size_t>(t) * kQueryHeads + h) * kHeadDim;
+            OutT *srow = stage + (ct * kQueryBlock + kg_e * 4 + r) * kHeadDim + row_e;
 #pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    if constexpr (F32IO) p.out32[ooff + c * 16 + row_e] = o[ct][c][r] * inv;
-                    else p.out[ooff + c * 16 + row_e] = __builtin_bit_cast(uint16_t, to_h(o[ct][c][r] * inv));
-                }
+            for (int c = 0; c < 8; ++c) {
+                if constexpr (F32IO) srow[c * 16] = o[ct][c][r] * inv;
+                else srow[c * 16] = __builtin_bit_cast(uint16_t, to_h(o[ct][c][r] * inv));
             }
         }
     }
+    __builtin_amdgcn_wave_barrier();  // the wave reads what its other lanes wrote (LDS is in order per wave)
+    constexpr int kChunks = 2 * kQueryBlock * kHeadDim / kChunk;  // of the wave: 512 (fp16) or 1024 (f32)
+#pragma unroll
+    for (int j = 0; j < kChunks / 64; ++j) {
+        const int q = j * 64 + lane_e;                   // chunk: [head][token][chunk of the row]
+        const int ct = q / (kQueryBlock * kHeadDim / kChunk);
+        const int tt = (q / (kHeadDim / kChunk)) % kQueryBlock, d0 = (q % (kHeadDim / kChunk)) * kChunk;
+        const int t = t0 + tt, h = static_cast<int>(g) * kGroup + wave * 2 + ct;
+        if (t < n) {
+            const float4_t v = *reinterpret_cast<const float4_t *>(stage + (ct * kQueryBlock + tt) * kHeadDim + d0);
+            OutT *dst = (F32IO ? reinterpret_cast<OutT *>(p.out32) : reinterpret_cast<OutT *>(p.out)) +
+                        (static_cast<size_t>(t) * kQueryHeads + h) * kHeadDim + d0;
+            *reinterpret_cast<float4_t *>(dst) = v;
+        }
+    }
+    // Every wave has read its staged outputs before the next segment loads
+    // its first stages into these buffers.
+    __syncthreads();
   };
   // a light block, then part of a heavy one (two inlined copies: each is
   // register-allocated like a single segment)

@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "pvlc_device.hpp"
 #include "pvlc_internal.hpp"
@@ -148,9 +149,44 @@ __global__ __launch_bounds__(kSplitThreads) void projection_split_kernel(const f
 __device__ inline int a_offset(int kchunk, int row) { return (kchunk * kTileM + row) * 8; }
 __device__ inline int w_offset(int kchunk, int row) { return (row * 4 + (kchunk ^ ((row >> 1) & 3))) * 8; }
 
-__global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_kernel(
+// Ring stage u of the narrow GEMM: distinct LDS arrays per stage (one
+// function-scope array per instantiation), so the compiler sees that loads
+// into one stage and fragment reads of another do not alias and adds no wait
+// of its own before the reads.
+template <int U> __device__ __forceinline__ uint16_t *ring_a() {
+    __shared__ uint16_t buf[kBlockElems];
+    return buf;
+}
+template <int U> __device__ __forceinline__ uint16_t *ring_w() {
+    __shared__ uint16_t buf[kTileElems];
+    return buf;
+}
+// Calls f(integral_constant<U>) for U = B .. E-1 (compile-time ring indices).
+template <int B, int E> struct StageUnroll {
+    template <class F> __device__ __forceinline__ static void run(F &&f) {
+        f(std::integral_constant<int, B>{});
+        StageUnroll<B + 1, E>::run(f);
+    }
+};
+template <int E> struct StageUnroll<E, E> {
+    template <class F> __device__ __forceinline__ static void run(F &&) {}
+};
+
+// STAGES-deep ring of (activation block, weight tile) stages, 24 KiB each:
+// step s computes stage s while the loads of stages s+1 .. s+STAGES-1 are in
+// flight, and its closing barrier waits only for stage s+1 (vmcnt(6 (STAGES -
+// 2)): the 6 loads per thread of each later stage may still be outstanding).
+// Three stages (72 KiB) leave room for two workgroups per compute unit; six
+// (144 KiB) are for launches of at most one workgroup per compute unit, where
+// nothing else on the unit covers the load latency (an L2 miss served by the
+// Infinity Cache takes longer than two steps of MFMAs).
+template <int STAGES, int MIN_WGS>
+__global__ __launch_bounds__(kGemmThreads, MIN_WGS) void projection_gemm_kernel(
     const uint16_t *__restrict__ tiles, const int32_t *__restrict__ exponents, const uint16_t *__restrict__ weight,
     const float *__restrict__ bias, float *__restrict__ out, uint32_t rows, uint32_t k_width, uint32_t n_width) {
+    static_assert(STAGES >= 3 && 6 * (STAGES - 1) <= 63, "vmcnt holds at most 63 outstanding loads");
+    constexpr int kWaitRing = 0x0F70 | (6 * (STAGES - 2) & 15) | ((6 * (STAGES - 2) >> 4) << 14);
+    constexpr int kWaitRingPrologue = 0x0F70 | (6 * (STAGES - 1) & 15) | ((6 * (STAGES - 1) >> 4) << 14);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int row16 = lane & 15, kg = lane >> 4;
@@ -165,18 +201,6 @@ __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_kernel(
     const uint32_t mt = tile / n_tiles, m0 = mt * kTileM, n0 = (tile % n_tiles) * kTileN;
     const int wm = wave >> 1, wn = wave & 1;  // the wave's 64 x 64 quadrant
     const uint32_t steps = k_width / kTileK;
-
-    // Three-stage ring of distinct LDS arrays (picked at compile time in the
-    // loop unrolled by three): step s computes stage s while the loads of
-    // stage s+1 and s+2 are in flight, and its closing barrier waits only for
-    // stage s+1 (vmcnt(6): the 6 loads per thread of stage s+2 may still be
-    // outstanding).  Loads of stage 1 and of stage s+2 beyond the last clamp
-    // to the last stage, so a single-step K is also exact.  The compiler sees
-    // that loads into one array and reads of another do not alias, so it adds
-    // no wait of its own before the reads.
-    __shared__ uint16_t sa0[kBlockElems], sw0[kTileElems];
-    __shared__ uint16_t sa1[kBlockElems], sw1[kTileElems];
-    __shared__ uint16_t sa2[kBlockElems], sw2[kTileElems];
     typedef __attribute__((address_space(3))) void *lds_ptr;
 
     // Direct global-to-LDS loads, 64 lanes x 16 bytes per instruction, lane l
@@ -213,56 +237,95 @@ __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_kernel(
 
     // 16 x 16 x 32 tiles: A = activations (lane row = l % 16, k = (l / 16) * 8 ..),
     // B = W^T (lane column = l % 16, same k), C: column l % 16, rows (l / 16) * 4 + i.
-    auto compute = [&](const uint16_t *sa, const uint16_t *sw) {
-        half8_t bf[4];
+    // A step's 12 fragments (4 weight, 4 hi, 4 lo) are read from LDS during
+    // the previous step's MFMAs (two register sets).
+    struct Frags {
+        half8_t b[4], h[4], l[4];
+    };
+    auto read_frags = [&](Frags &f, const uint16_t *sa, const uint16_t *sw) {
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
-            bf[cb] = *reinterpret_cast<const half8_t *>(sw + w_offset(kg, wn * 64 + cb * 16 + row16));
+            f.b[cb] = *reinterpret_cast<const half8_t *>(sw + w_offset(kg, wn * 64 + cb * 16 + row16));
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             const int trow = wm * 64 + rb * 16 + row16;
-            const half8_t ah = *reinterpret_cast<const half8_t *>(sa + a_offset(kg, trow));
-            const half8_t al = *reinterpret_cast<const half8_t *>(sa + kTileElems + a_offset(kg, trow));
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
-                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bf[cb], acc[rb][cb], 0, 0, 0);
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
-                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[cb], acc[rb][cb], 0, 0, 0);
+            f.h[rb] = *reinterpret_cast<const half8_t *>(sa + a_offset(kg, trow));
+            f.l[rb] = *reinterpret_cast<const half8_t *>(sa + kTileElems + a_offset(kg, trow));
         }
-        // Schedule: the 12 fragment reads first, then the 32 MFMAs with the
-        // step's 6 global-to-LDS loads spread among them (masks: 0x100 LDS
-        // read, 0x008 MFMA, 0x020 global load).
-        __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+    };
+    auto mfmas = [&](const Frags &f) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.h[rb], f.b[cb], acc[rb][cb], 0, 0, 0);
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+                acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.l[rb], f.b[cb], acc[rb][cb], 0, 0, 0);
+        }
+    };
+    // Step s (ring slot U = s % STAGES), entered with stage s's fragments in
+    // registers: wait for this thread's loads of stage s+1, finish its
+    // fragment reads of stage s, barrier (every wave's stage s+1 has landed
+    // and nobody reads slot U any more); load stage s+STAGES into slot U
+    // (past the end: the last stage again, never read); then stage s's 32
+    // MFMAs with stage s+1's 12 fragment reads and the 6 loads spread among
+    // them (sched_group_barrier masks: 0x008 MFMA, 0x100 LDS read, 0x020
+    // global load).  Unconditional loads keep the waits exact.
+    Frags fa, fb;
+    uint32_t s = 0;
+    auto step = [&](auto uc, Frags &cur, Frags &nxt) {
+        constexpr int U = decltype(uc)::value, N = (U + 1) % STAGES;
+        __builtin_amdgcn_s_waitcnt(kWaitRing & ~0x0F00);  // ... and lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        stage(min(s + U + STAGES, steps - 1), ring_a<U>(), ring_w<U>());
+        read_frags(nxt, ring_a<N>(), ring_w<N>());
+        mfmas(cur);
 #pragma unroll
         for (int i = 0; i < 6; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     };
-    // Step s: load stage s+2 (past the end: the last stage again, into the
-    // buffer step s-1 freed, never read), compute stage s, wait for stage s+1,
-    // barrier.  Unconditional loads keep the waits exact.
-    auto step = [&](uint32_t s, uint16_t *ca, uint16_t *cw, uint16_t *na, uint16_t *nw) {
-        stage(min(s + 2, steps - 1), na, nw);
-        compute(ca, cw);
-        __builtin_amdgcn_s_waitcnt(kWaitVm6);
-        __builtin_amdgcn_s_barrier();
-    };
-
-    stage(0, sa0, sw0);
-    stage(min(1u, steps - 1), sa1, sw1);
-    __builtin_amdgcn_s_waitcnt(kWaitVm6);
+    // Prologue: stages 0 .. STAGES-1 into every slot, wait for stage 0 (the
+    // other STAGES-1 stages' loads may be outstanding), read its fragments.
+    StageUnroll<0, STAGES>::run([&](auto uc) {
+        constexpr int U = decltype(uc)::value;
+        stage(min(static_cast<uint32_t>(U), steps - 1), ring_a<U>(), ring_w<U>());
+    });
+    __builtin_amdgcn_s_waitcnt(kWaitRingPrologue);
     __builtin_amdgcn_s_barrier();
-    uint32_t s = 0;
-    for (; s + 3 <= steps; s += 3) {
-        step(s, sa0, sw0, sa2, sw2);
-        step(s + 1, sa1, sw1, sa0, sw0);
-        step(s + 2, sa2, sw2, sa1, sw1);
+    read_frags(fa, ring_a<0>(), ring_w<0>());
+    // Unrolled by 2 STAGES: the ring slot and the register set are both
+    // compile-time in every step.
+    for (; s + 2 * STAGES <= steps; s += 2 * STAGES) {
+        StageUnroll<0, STAGES>::run([&](auto uc) {
+            if constexpr (decltype(uc)::value % 2 == 0) step(uc, fa, fb); else step(uc, fb, fa);
+        });
+        s += STAGES;
+        StageUnroll<0, STAGES>::run([&](auto uc) {
+            if constexpr ((decltype(uc)::value + STAGES) % 2 == 0) step(uc, fa, fb); else step(uc, fb, fa);
+        });
+        s -= STAGES;
     }
-    if (s < steps) step(s, sa0, sw0, sa2, sw2);
-    if (s + 1 < steps) step(s + 1, sa1, sw1, sa0, sw0);
+    // The remaining < 2 STAGES steps (the fragments of stage s are in fa).
+    StageUnroll<0, STAGES>::run([&](auto uc) {
+        if (s + decltype(uc)::value < steps) {
+            if constexpr (decltype(uc)::value % 2 == 0) step(uc, fa, fb); else step(uc, fb, fa);
+        }
+    });
+    if (s + STAGES < steps) {
+        s += STAGES;
+        StageUnroll<0, STAGES - 1>::run([&](auto uc) {
+            if (s + decltype(uc)::value < steps) {
+                if constexpr ((decltype(uc)::value + STAGES) % 2 == 0) step(uc, fa, fb); else step(uc, fb, fa);
+            }
+        });
+    }
     __builtin_amdgcn_s_waitcnt(kWaitVm0);  // no load into LDS outlives the loop
 
     // Epilogue: x 2^e of the row (exact), + bias, f32 stores.
@@ -522,8 +585,13 @@ int launch_linear_projection_f16(const float *input, const uint16_t *weight, con
         return static_cast<int>(hipGetLastError());
     }
     const uint32_t tiles = (n_width / kTileN + (n_width % kTileN != 0)) * m_tiles;  // < 2^24 (checked by the caller)
-    hipLaunchKernelGGL(projection_gemm_kernel, dim3(tiles), dim3(kGemmThreads), 0, st, ws.tiles, ws.exponents, weight,
-                       bias, out, rows, k_width, n_width);
+    if (tiles <= kTargetWorkgroups)
+        // One workgroup per compute unit at most: the six-stage ring.
+        hipLaunchKernelGGL((projection_gemm_kernel<6, 1>), dim3(tiles), dim3(kGemmThreads), 0, st, ws.tiles,
+                           ws.exponents, weight, bias, out, rows, k_width, n_width);
+    else
+        hipLaunchKernelGGL((projection_gemm_kernel<3, 2>), dim3(tiles), dim3(kGemmThreads), 0, st, ws.tiles,
+                           ws.exponents, weight, bias, out, rows, k_width, n_width);
     return static_cast<int>(hipGetLastError());
 }
 

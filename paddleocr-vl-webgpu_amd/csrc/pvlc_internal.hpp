@@ -189,8 +189,13 @@ int launch_linear_projection_f16(const float *input, const uint16_t *weight, con
 // first runs the light block, then the first k steps of the heavy one; the
 // second runs the rest of the heavy block (which holds the diagonal), and the
 // one that finishes last merges the two parts.  Used when the longest block
-// is longer than kPrefillSplitSteps.
+// is longer than kPrefillSplitSteps.  A pair whose light workgroup would take
+// fewer than kPrefillSplitMin heavy steps is not split (the light block and
+// the heavy block run whole on the two workgroups): a second segment costs
+// its workgroup a query load, a pipeline fill and the partial hand-off, about
+// what 4 to 5 steps cost (measured at N=4096: 9-13 us for 1-2 steps).
 constexpr uint32_t kPrefillSplitSteps = 32;
+constexpr uint32_t kPrefillSplitMin = 5;
 constexpr uint32_t kPrefillPartialFloats = 4 * 64 * 74;  // 4 waves x 64 lanes x (2 x 9 x 4 O/l + 2 m)
 
 constexpr uint32_t prefill_block_steps(uint32_t qb) { return qb / 4 + 1; }
@@ -211,7 +216,8 @@ constexpr uint32_t prefill_pair_segments(uint32_t w, uint32_t qblocks, uint32_t 
     *pair = pg >> 1;
     const uint32_t heavy = qblocks - 1u - *pair, light = *pair;
     const uint32_t sh = prefill_block_steps(heavy), sl = light == heavy ? 0u : prefill_block_steps(light);
-    const uint32_t k = (sh - sl + 1u) / 2u;  // heavy steps the light block's workgroup takes
+    const uint32_t half = (sh - sl + 1u) / 2u;
+    const uint32_t k = half < kPrefillSplitMin ? 0u : half;  // heavy steps the light block's workgroup takes
     // Straight-line assignments (no runtime-indexed pointer), so that on the
     // device both segments stay in registers.  sh >= 1, so k >= sh implies k > 0.
     PrefillSegment s0{}, s1{};

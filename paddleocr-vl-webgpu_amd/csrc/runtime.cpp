@@ -847,6 +847,16 @@ pvlc_hip_status prefill_checked(const pvlc_hip_paged_prefill_args *args, void *s
     }
     if (!args->key_cache || !args->value_cache)
         return invalid(PVLC_HIP_INV_LENGTH_MISMATCH, "prefill buffer pointer is NULL");
+    {
+        // The kernels move query, key, value, output and cache rows as 16-byte vectors.
+        const void *rows[] = {args->query, args->key, args->value, args->out, args->key_cache, args->value_cache,
+                              args->query_scratch, f32 ? f32->query : nullptr, f32 ? f32->key : nullptr,
+                              f32 ? f32->value : nullptr, f32 ? f32->out : nullptr};
+        for (const void *r : rows)
+            if (reinterpret_cast<uintptr_t>(r) % 16 != 0)
+                return invalid(PVLC_HIP_INV_LENGTH_MISMATCH,
+                               "prefill query, key, value, output, cache and scratch must be 16-byte aligned");
+    }
     if ((args->rope_cos == nullptr) != (args->rope_sin == nullptr) || (args->rope_cos && args->rope_rows == 0))
         return invalid(PVLC_HIP_INV_INVALID_ROTARY_DIMENSION, "rotary tables must be given together with rows");
     if (!args->positions && args->rope_cos && args->tokens > args->rope_rows)

@@ -347,3 +347,19 @@ def test_f32_operand_prefill_rejects_mixed_or_missing_operands():
         pvlc.paged_prefill_f16(tokens=16, num_blocks=1, key_cache=fake, value_cache=fake, query=None, key=None,
                                value=None, out=None)
     assert code(e) == ("InvalidInvocation", "LengthMismatch")
+
+
+def test_prefill_rejects_unaligned_rows():
+    """The prefill kernels move query, key, value, output, cache and scratch rows as 16-byte vectors: a pointer off
+    that alignment is rejected before any GPU effect (placeholder addresses, never read)."""
+    fake = 1 << 20
+    base = dict(tokens=16, num_blocks=1, key_cache=fake, value_cache=fake, query=fake, key=fake, value=fake, out=fake)
+    for name in ("query", "key", "value", "out", "key_cache", "value_cache", "query_scratch"):
+        kw = dict(base, **{name: fake + 2})
+        with pytest.raises(pvlc.PvlcHipError) as e:
+            pvlc.paged_prefill_f16(**kw)
+        assert code(e) == ("InvalidInvocation", "LengthMismatch") and "16-byte aligned" in str(e.value), name
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.paged_prefill_f32io(tokens=16, num_blocks=1, key_cache=fake, value_cache=fake, query=fake, key=fake + 4,
+                                 value=fake, out=fake)
+    assert "16-byte aligned" in str(e.value)
