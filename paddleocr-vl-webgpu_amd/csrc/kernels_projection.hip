@@ -47,7 +47,7 @@ constexpr int kBlockElems = 2 * kTileElems;  // one activation block: hi and lo 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0, expcnt 6:4, lgkmcnt
 // 11:8, the last two left at their maximum) -- as builtins, so the compiler's
 // own wait insertion knows which loads they retire.
-constexpr int kWaitVm6 = 0x0F76, kWaitVm4 = 0x0F74, kWaitVm0 = 0x0F70;  // vmcnt(6) / vmcnt(4) / vmcnt(0)
+constexpr int kWaitVm4 = 0x0F74, kWaitVm0 = 0x0F70;  // vmcnt(4) / vmcnt(0)
 
 // Exponent e of a row whose largest magnitude is m: m * 2^-e in [2^13, 2^14)
 // (0 for an all-zero row).
@@ -154,11 +154,11 @@ __device__ inline int w_offset(int kchunk, int row) { return (row * 4 + (kchunk 
 // into one stage and fragment reads of another do not alias and adds no wait
 // of its own before the reads.
 template <int U> __device__ __forceinline__ uint16_t *ring_a() {
-    __shared__ uint16_t buf[kBlockElems];
+    __shared__ __align__(16) uint16_t buf[kBlockElems];
     return buf;
 }
-template <int U> __device__ __forceinline__ uint16_t *ring_w() {
-    __shared__ uint16_t buf[kTileElems];
+template <int U, int NT> __device__ __forceinline__ uint16_t *ring_w() {
+    __shared__ __align__(16) uint16_t buf[NT * kTileK];
     return buf;
 }
 // Calls f(integral_constant<U>) for U = B .. E-1 (compile-time ring indices).
@@ -172,21 +172,27 @@ template <int E> struct StageUnroll<E, E> {
     template <class F> __device__ __forceinline__ static void run(F &&) {}
 };
 
-// STAGES-deep ring of (activation block, weight tile) stages, 24 KiB each:
+// 128 x NT output tiles (NT = 128 or 160 columns), 4 waves of 64 x NT/2.
+// STAGES-deep ring of (activation block 16 KiB, weight tile NT x 32) stages:
 // step s computes stage s while the loads of stages s+1 .. s+STAGES-1 are in
-// flight, and its closing barrier waits only for stage s+1 (vmcnt(6 (STAGES -
-// 2)): the 6 loads per thread of each later stage may still be outstanding).
-// Three stages (72 KiB) leave room for two workgroups per compute unit; six
-// (144 KiB) are for launches of at most one workgroup per compute unit, where
-// nothing else on the unit covers the load latency (an L2 miss served by the
-// Infinity Cache takes longer than two steps of MFMAs).
-template <int STAGES, int MIN_WGS>
+// flight.  Three stages (72 or 78 KiB) leave room for two workgroups per
+// compute unit; six (144 KiB, NT = 128) are for launches of at most one
+// workgroup per compute unit, where nothing else on the unit covers the load
+// latency.  NT = 160 serves widths that are multiples of 160 with as many
+// tiles as two workgroups per compute unit hold (q|k|v at N=4096: 512 tiles in
+// one round, against 640 tiles of 128 that leave a second round a quarter
+// full).
+template <int STAGES, int MIN_WGS, int NT>
 __global__ __launch_bounds__(kGemmThreads, MIN_WGS) void projection_gemm_kernel(
     const uint16_t *__restrict__ tiles, const int32_t *__restrict__ exponents, const uint16_t *__restrict__ weight,
     const float *__restrict__ bias, float *__restrict__ out, uint32_t rows, uint32_t k_width, uint32_t n_width) {
-    static_assert(STAGES >= 3 && 6 * (STAGES - 1) <= 63, "vmcnt holds at most 63 outstanding loads");
-    constexpr int kWaitRing = 0x0F70 | (6 * (STAGES - 2) & 15) | ((6 * (STAGES - 2) >> 4) << 14);
-    constexpr int kWaitRingPrologue = 0x0F70 | (6 * (STAGES - 1) & 15) | ((6 * (STAGES - 1) >> 4) << 14);
+    static_assert(NT == 128 || NT == 160, "column tile of 128 or 160");
+    constexpr int CB = NT / 32;                 // 16-column MFMA tiles per wave
+    constexpr int kWLoads = NT == 128 ? 2 : 3;  // weight loads per thread and stage
+    constexpr int kLoads = 4 + kWLoads;         // loads per thread and stage
+    static_assert(STAGES >= 3 && kLoads * (STAGES - 1) <= 63, "vmcnt holds at most 63 outstanding loads");
+    constexpr int kWaitRing = 0x0F70 | (kLoads * (STAGES - 2) & 15) | ((kLoads * (STAGES - 2) >> 4) << 14);
+    constexpr int kWaitRingPrologue = 0x0F70 | (kLoads * (STAGES - 1) & 15) | ((kLoads * (STAGES - 1) >> 4) << 14);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int row16 = lane & 15, kg = lane >> 4;
@@ -194,27 +200,35 @@ __global__ __launch_bounds__(kGemmThreads, MIN_WGS) void projection_gemm_kernel(
     // XCDs, so workgroup b runs on XCD b % 8; the permutation below gives XCD
     // x a contiguous range of tiles in row-major order (whole bands of output
     // rows), and the L2 of that XCD serves every column tile of its rows.
-    const uint32_t n_tiles = n_width / kTileN + (n_width % kTileN != 0);
+    const uint32_t n_tiles = n_width / NT + (n_width % NT != 0);
     const uint32_t total = gridDim.x, xcd = blockIdx.x % kXcds, idx = blockIdx.x / kXcds;
     const uint32_t q = total / kXcds, r = total % kXcds;
     const uint32_t tile = xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
-    const uint32_t mt = tile / n_tiles, m0 = mt * kTileM, n0 = (tile % n_tiles) * kTileN;
-    const int wm = wave >> 1, wn = wave & 1;  // the wave's 64 x 64 quadrant
+    const uint32_t mt = tile / n_tiles, m0 = mt * kTileM, n0 = (tile % n_tiles) * NT;
+    const int wm = wave >> 1, wn = wave & 1;  // the wave's 64 x NT/2 part
     const uint32_t steps = k_width / kTileK;
     typedef __attribute__((address_space(3))) void *lds_ptr;
 
     // Direct global-to-LDS loads, 64 lanes x 16 bytes per instruction, lane l
     // landing at 16 l of the instruction's 1 KiB.  Activations: the 16 KiB
     // block (tile mt, step s) as 16 instructions of 1 KiB, 4 per wave.
-    // Weights: 8 instructions of 16 rows each, 2 per wave; lane l of
-    // instruction j fills LDS slot p = 64 j + l, i.e. row p / 4, slot p % 4.
-    // Weight rows past the end re-read the last row (never stored).
+    // Weights: NT / 16 instructions of 16 rows each; lane l of instruction j
+    // fills LDS slot p = 64 j + l, i.e. row p / 4, slot p % 4.  Wave w issues
+    // instructions 2w and 2w+1 and, for NT = 160, instruction 8 + (w & 1) (so
+    // waves 2 and 3 repeat waves 0 and 1's: the same bytes into the same
+    // place, and every wave counts the same loads).  Weight rows past the end
+    // re-read the last row (never stored).
     const uint16_t *a_tiles = tiles + static_cast<size_t>(mt) * steps * kBlockElems + (wave * 4) * 512 + lane * 8;
     const uint32_t last_col = n_width - 1;
-    size_t w_row_off[2];
+    // (Fixed-size arrays: hipcc's host pass drops the kernel's launch stub,
+    // without a diagnostic, when a lambda called from the generic step lambda
+    // captures a local array whose size depends on the template arguments.)
+    int w_inst[3];
+    size_t w_row_off[3];
 #pragma unroll
-    for (int rw = 0; rw < 2; ++rw) {
-        const int p = 64 * (wave * 2 + rw) + lane, wrow = p >> 2;
+    for (int rw = 0; rw < kWLoads; ++rw) {
+        w_inst[rw] = rw < 2 ? wave * 2 + rw : 8 + (wave & 1);
+        const int p = 64 * w_inst[rw] + lane, wrow = p >> 2;
         const int kc = (p & 3) ^ ((wrow >> 1) & 3);
         w_row_off[rw] = static_cast<size_t>(min(n0 + wrow, last_col)) * k_width + kc * 8;
     }
@@ -224,28 +238,28 @@ __global__ __launch_bounds__(kGemmThreads, MIN_WGS) void projection_gemm_kernel(
         for (int j = 0; j < 4; ++j)
             __builtin_amdgcn_global_load_lds(a + j * 512, (lds_ptr)(da + (wave * 4 + j) * 512), 16, 0, 0);
 #pragma unroll
-        for (int rw = 0; rw < 2; ++rw)
+        for (int rw = 0; rw < kWLoads; ++rw)
             __builtin_amdgcn_global_load_lds(weight + w_row_off[rw] + s * kTileK,
-                                             (lds_ptr)(dw + (wave * 2 + rw) * 512), 16, 0, 0);
+                                             (lds_ptr)(dw + w_inst[rw] * 512), 16, 0, 0);
     };
 
-    float4_t acc[4][4];
+    float4_t acc[4][CB];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < CB; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     // 16 x 16 x 32 tiles: A = activations (lane row = l % 16, k = (l / 16) * 8 ..),
     // B = W^T (lane column = l % 16, same k), C: column l % 16, rows (l / 16) * 4 + i.
-    // A step's 12 fragments (4 weight, 4 hi, 4 lo) are read from LDS during
-    // the previous step's MFMAs (two register sets).
+    // A step's 8 + CB fragments (CB weight, 4 hi, 4 lo) are read from LDS
+    // during the previous step's MFMAs (two register sets).
     struct Frags {
-        half8_t b[4], h[4], l[4];
+        half8_t b[CB], h[4], l[4];
     };
     auto read_frags = [&](Frags &f, const uint16_t *sa, const uint16_t *sw) {
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-            f.b[cb] = *reinterpret_cast<const half8_t *>(sw + w_offset(kg, wn * 64 + cb * 16 + row16));
+        for (int cb = 0; cb < CB; ++cb)
+            f.b[cb] = *reinterpret_cast<const half8_t *>(sw + w_offset(kg, wn * (NT / 2) + cb * 16 + row16));
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             const int trow = wm * 64 + rb * 16 + row16;
@@ -257,10 +271,10 @@ __global__ __launch_bounds__(kGemmThreads, MIN_WGS) void projection_gemm_kernel(
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
+            for (int cb = 0; cb < CB; ++cb)
                 acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.h[rb], f.b[cb], acc[rb][cb], 0, 0, 0);
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
+            for (int cb = 0; cb < CB; ++cb)
                 acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.l[rb], f.b[cb], acc[rb][cb], 0, 0, 0);
         }
     };
@@ -268,38 +282,53 @@ __global__ __launch_bounds__(kGemmThreads, MIN_WGS) void projection_gemm_kernel(
     // registers: wait for this thread's loads of stage s+1, finish its
     // fragment reads of stage s, barrier (every wave's stage s+1 has landed
     // and nobody reads slot U any more); load stage s+STAGES into slot U
-    // (past the end: the last stage again, never read); then stage s's 32
-    // MFMAs with stage s+1's 12 fragment reads and the 6 loads spread among
-    // them (sched_group_barrier masks: 0x008 MFMA, 0x100 LDS read, 0x020
-    // global load).  Unconditional loads keep the waits exact.
+    // (past the end: the last stage again, never read); then stage s's 8 CB
+    // MFMAs with stage s+1's 8 + CB fragment reads and the kLoads loads
+    // spread among them (sched_group_barrier masks: 0x008 MFMA, 0x100 LDS
+    // read, 0x020 global load).  Unconditional loads keep the waits exact.
     Frags fa, fb;
     uint32_t s = 0;
     auto step = [&](auto uc, Frags &cur, Frags &nxt) {
         constexpr int U = decltype(uc)::value, N = (U + 1) % STAGES;
         __builtin_amdgcn_s_waitcnt(kWaitRing & ~0x0F00);  // ... and lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
-        stage(min(s + U + STAGES, steps - 1), ring_a<U>(), ring_w<U>());
-        read_frags(nxt, ring_a<N>(), ring_w<N>());
+        stage(min(s + U + STAGES, steps - 1), ring_a<U>(), ring_w<U, NT>());
+        read_frags(nxt, ring_a<N>(), ring_w<N, NT>());
         mfmas(cur);
+        if constexpr (NT == 128) {
 #pragma unroll
-        for (int i = 0; i < 6; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            for (int i = 0; i < 6; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 6; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 7, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     };
     // Prologue: stages 0 .. STAGES-1 into every slot, wait for stage 0 (the
     // other STAGES-1 stages' loads may be outstanding), read its fragments.
     StageUnroll<0, STAGES>::run([&](auto uc) {
         constexpr int U = decltype(uc)::value;
-        stage(min(static_cast<uint32_t>(U), steps - 1), ring_a<U>(), ring_w<U>());
+        stage(min(static_cast<uint32_t>(U), steps - 1), ring_a<U>(), ring_w<U, NT>());
     });
     __builtin_amdgcn_s_waitcnt(kWaitRingPrologue);
     __builtin_amdgcn_s_barrier();
-    read_frags(fa, ring_a<0>(), ring_w<0>());
+    read_frags(fa, ring_a<0>(), ring_w<0, NT>());
     // Unrolled by 2 STAGES: the ring slot and the register set are both
     // compile-time in every step.
     for (; s + 2 * STAGES <= steps; s += 2 * STAGES) {
@@ -337,8 +366,8 @@ __global__ __launch_bounds__(kGemmThreads, MIN_WGS) void projection_gemm_kernel(
             if (r >= rows) continue;
             const int e = exponents[r];
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-                const uint32_t n = n0 + wn * 64 + cb * 16 + row16;
+            for (int cb = 0; cb < CB; ++cb) {
+                const uint32_t n = n0 + wn * (NT / 2) + cb * 16 + row16;
                 if (n < n_width) out[static_cast<size_t>(r) * n_width + n] = __builtin_ldexpf(acc[rb][cb][i], e) + bias[n];
             }
         }
@@ -585,13 +614,20 @@ int launch_linear_projection_f16(const float *input, const uint16_t *weight, con
         return static_cast<int>(hipGetLastError());
     }
     const uint32_t tiles = (n_width / kTileN + (n_width % kTileN != 0)) * m_tiles;  // < 2^24 (checked by the caller)
-    if (tiles <= kTargetWorkgroups)
+    const uint32_t tiles160 = (n_width / 160 + (n_width % 160 != 0)) * m_tiles;
+    if (tiles <= kTargetWorkgroups) {
         // One workgroup per compute unit at most: the six-stage ring.
-        hipLaunchKernelGGL((projection_gemm_kernel<6, 1>), dim3(tiles), dim3(kGemmThreads), 0, st, ws.tiles,
+        hipLaunchKernelGGL((projection_gemm_kernel<6, 1, 128>), dim3(tiles), dim3(kGemmThreads), 0, st, ws.tiles,
                            ws.exponents, weight, bias, out, rows, k_width, n_width);
-    else
-        hipLaunchKernelGGL((projection_gemm_kernel<3, 2>), dim3(tiles), dim3(kGemmThreads), 0, st, ws.tiles,
+    } else if (n_width % 160 == 0 && tiles160 <= 2 * kTargetWorkgroups && tiles > 2 * kTargetWorkgroups) {
+        // 160-column tiles fit one round of two workgroups per compute unit
+        // where 128-column tiles need a second.
+        hipLaunchKernelGGL((projection_gemm_kernel<3, 2, 160>), dim3(tiles160), dim3(kGemmThreads), 0, st, ws.tiles,
                            ws.exponents, weight, bias, out, rows, k_width, n_width);
+    } else {
+        hipLaunchKernelGGL((projection_gemm_kernel<3, 2, 128>), dim3(tiles), dim3(kGemmThreads), 0, st, ws.tiles,
+                           ws.exponents, weight, bias, out, rows, k_width, n_width);
+    }
     return static_cast<int>(hipGetLastError());
 }
 

@@ -126,3 +126,33 @@ def test_wide_kernel_writes_every_tile(rows, k, n):
     ratio = bound_ratio(got[sel], wf, x[sel], b, 2 * k + 2, True)
     log(f"[parity] wide projection {rows}x{k}x{n}: {len(sel)} rows, max |gpu - f64| / bound = {ratio:.3f}")
     assert ratio <= 1.0
+
+
+@pytest.mark.parametrize("rows,k,n", [(4096, 1024, 2560),   # q|k|v at N=4096: 512 tiles of 128 x 160, one round
+                                      (4000, 256, 2560),    # ragged last row tile
+                                      (3000, 64, 3200)])    # 2 k steps: the ring's prologue and tail only
+def test_160_column_tiles_write_every_output(rows, k, n):
+    """Widths that are multiples of 160 with more than 512 tiles of 128 x 128 but at most 512 of 128 x 160 run the
+    160-column GEMM (its weight loads: waves 2 and 3 repeat waves 0 and 1's third load): every output element is
+    written and the first and last rows of every row tile are within the f64 bound over all columns."""
+    import torch
+    log(f"case: 160-column projection rows={rows} k={k} n={n}")
+    seed = rows * 3 + k + n
+    w = f16_bits(seed, n * k, 0.05)
+    x = O.normal_f32(seed + 1, rows * k).reshape(rows, k)
+    b = O.normal_f32(seed + 2, n)
+    wsb = pvlc.linear_projection_workspace_bytes(rows, k)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    d_out = torch.full((rows * n + 64,), float("nan"), dtype=torch.float32, device="cuda")
+    pvlc.linear_projection_f16(to_dev_f32(x), to_dev(w), to_dev_f32(b), d_out, rows, k, n, ws, wsb)
+    torch.cuda.synchronize()
+    got = d_out.cpu().numpy()
+    assert np.all(np.isnan(got[rows * n:])), "projection wrote past the output"
+    got = got[:rows * n].reshape(rows, n)
+    assert np.all(np.isfinite(got)), f"{int(np.sum(~np.isfinite(got)))} outputs never written"
+    sel = sorted({r for t in range(0, rows, 128) for r in (t, min(t + 127, rows - 1))})
+    wf = widen(w).reshape(n, k)
+    ratio = bound_ratio(got[sel], wf, x[sel], b, 2 * k + 2, True)
+    log(f"[parity] 160-column projection {rows}x{k}x{n}: {len(sel)} rows, max |gpu - f64| / bound = {ratio:.3f}")
+    assert ratio <= 1.0
+
