@@ -268,15 +268,20 @@ typedef struct pvlc_hip_kv_step_execution {
 
 /* NativeDecoderKvSession::step, decoder_kv_session.rs:499-529: append the
  * (already rotated) key/value row at cache_tokens, attend over cache_tokens+1
- * rows, write query_heads*head_dim f32 to attention.  An invalid step has no
+ * rows, write query_heads*head_dim f32 to attention.  The GPU rounds the
+ * query, key and value to fp16 once (RNE) and attends over the fp16 cache; the
+ * session keeps the f32 row as given for finish.  An invalid step has no
  * effect; a failure after submission poisons the session terminally. */
 pvlc_hip_status pvlc_hip_kv_session_step(pvlc_hip_kv_session *session, const pvlc_hip_kv_step_operands *step,
                                          float *attention, size_t attention_len,
                                          pvlc_hip_kv_step_execution *execution_out);
 
 /* NativeDecoderKvSession::finish, decoder_kv_session.rs:531-545, :812-925:
- * read the full physical planes back.  Consumes the session: it is freed
- * whether or not the call succeeds, like Rust's `finish(self)`. */
+ * read the full physical planes back and return the capacity rows as given
+ * (the descriptor's, then each committed step's), bit for bit, once each is
+ * checked to match its fp16 row on the GPU (PVLC_HIP_OPERATION otherwise).
+ * Consumes the session: it is freed whether or not the call succeeds, like
+ * Rust's `finish(self)`. */
 pvlc_hip_status pvlc_hip_kv_session_finish(pvlc_hip_kv_session *session, float *key_cache, size_t key_cache_len,
                                            float *value_cache, size_t value_cache_len, uint32_t *cache_tokens_out,
                                            uint32_t *cache_capacity_out);

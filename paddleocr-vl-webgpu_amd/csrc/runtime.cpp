@@ -52,11 +52,15 @@ struct pvlc_hip_kv_session {
     uint32_t num_blocks = 0;
     uint16_t *key_cache = nullptr;    // blocked planes
     uint16_t *value_cache = nullptr;
-    uint16_t *step_operands = nullptr;  // device: query | key | value (fp16)
-    uint16_t *attention = nullptr;      // device: 16*128 fp16
+    float *step_operands = nullptr;  // device: query | key | value (f32, rounded to fp16 by the kernel)
+    float *attention = nullptr;      // device: 16*128 f32
     void *workspace = nullptr;
     size_t workspace_bytes = 0;
-    uint16_t *host_staging = nullptr;  // pinned: operands in, attention out
+    float *host_staging = nullptr;  // pinned: operands in, attention out
+    // Host: the rows exactly as given, compact [capacity][2][128] f32 (the
+    // descriptor's planes, then each committed step's appended row).  The
+    // device planes hold these rounded to fp16; finish returns these.
+    std::vector<float> key_rows, value_rows;
 };
 
 namespace {
@@ -132,7 +136,8 @@ void free_session_buffers(pvlc_hip_kv_session *s) {
     (void)hipFree(s->attention);
     (void)hipFree(s->workspace);
     (void)hipHostFree(s->host_staging);
-    s->key_cache = s->value_cache = s->step_operands = s->attention = nullptr;
+    s->key_cache = s->value_cache = nullptr;
+    s->step_operands = s->attention = nullptr;
     s->workspace = nullptr;
     s->host_staging = nullptr;
 }
@@ -310,16 +315,26 @@ pvlc_hip_status create_session(pvlc_hip_runtime *rt, const pvlc_hip_kv_session_p
     if ((e = hipSetDevice(rt->device)) != hipSuccess) return cleanup(hip_fail(e, "hipSetDevice"));
     if ((e = hipMalloc(&s->key_cache, plane_elems * 2)) != hipSuccess) return cleanup(hip_fail(e, "key cache"));
     if ((e = hipMalloc(&s->value_cache, plane_elems * 2)) != hipSuccess) return cleanup(hip_fail(e, "value cache"));
-    if ((e = hipMalloc(&s->step_operands, kStepElems * 2)) != hipSuccess) return cleanup(hip_fail(e, "operands"));
-    if ((e = hipMalloc(&s->attention, kQueryElems * 2)) != hipSuccess) return cleanup(hip_fail(e, "attention"));
+    if ((e = hipMalloc(&s->step_operands, kStepElems * 4)) != hipSuccess) return cleanup(hip_fail(e, "operands"));
+    if ((e = hipMalloc(&s->attention, kQueryElems * 4)) != hipSuccess) return cleanup(hip_fail(e, "attention"));
     if ((e = hipMalloc(&s->workspace, s->workspace_bytes)) != hipSuccess) return cleanup(hip_fail(e, "workspace"));
-    if ((e = hipHostMalloc(reinterpret_cast<void **>(&s->host_staging), (kStepElems + kQueryElems) * 2,
+    if ((e = hipHostMalloc(reinterpret_cast<void **>(&s->host_staging), (kStepElems + kQueryElems) * 4,
                            hipHostMallocDefault)) != hipSuccess)
         return cleanup(hip_fail(e, "pinned staging"));
 
-    // Initial planes: round to fp16 and scatter into the blocked layout on the
-    // host (rows past the capacity stay zero), then one copy per plane.
-    std::vector<uint16_t> kb(plane_elems, 0), vb(plane_elems, 0);
+    // Initial planes: keep the f32 rows, round to fp16 and scatter into the
+    // blocked layout on the host (rows past the capacity stay zero), then one
+    // copy per plane.
+    std::vector<uint16_t> kb, vb;
+    try {
+        const size_t rows_elems = static_cast<size_t>(plan.cache_capacity) * kRowElems;
+        s->key_rows.assign(key_cache, key_cache + rows_elems);
+        s->value_rows.assign(value_cache, value_cache + rows_elems);
+        kb.assign(plane_elems, 0);
+        vb.assign(plane_elems, 0);
+    } catch (const std::bad_alloc &) {
+        return cleanup(fail(PVLC_HIP_OUT_OF_MEMORY, PVLC_HIP_INV_NONE, "host copy of the cache rows"));
+    }
     for (uint32_t t = 0; t < plan.cache_capacity; ++t) {
         for (uint32_t h = 0; h < kKvHeads; ++h) {
             for (uint32_t d = 0; d < kHeadDim; ++d) {
@@ -350,12 +365,14 @@ pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_oper
                              pvlc_hip_kv_step_execution *exec) {
     pvlc_hip_runtime *rt = s->runtime;
     const uint64_t started = now_ns();
-    uint16_t *stage = s->host_staging;
-    pvlc_hip_f32_to_f16_host(step->query, stage, kQueryElems);
-    pvlc_hip_f32_to_f16_host(step->appended_key, stage + kQueryElems, kRowElems);
-    pvlc_hip_f32_to_f16_host(step->appended_value, stage + kQueryElems + kRowElems, kRowElems);
+    // The operands travel as f32; the kernel rounds the query, key and value
+    // to fp16 (RNE) and writes the attention as f32.
+    float *stage = s->host_staging;
+    std::memcpy(stage, step->query, kQueryElems * 4);
+    std::memcpy(stage + kQueryElems, step->appended_key, kRowElems * 4);
+    std::memcpy(stage + kQueryElems + kRowElems, step->appended_value, kRowElems * 4);
     HIP_TRY(hipSetDevice(rt->device), "hipSetDevice");
-    HIP_TRY(hipMemcpyAsync(s->step_operands, stage, kStepElems * 2, hipMemcpyHostToDevice, rt->stream),
+    HIP_TRY(hipMemcpyAsync(s->step_operands, stage, kStepElems * 4, hipMemcpyHostToDevice, rt->stream),
             "step operand upload");
     rt->counters.host_to_device_copies += 1;
 
@@ -369,19 +386,17 @@ pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_oper
     a.max_context = s->plan.cache_capacity;
     a.key_cache = s->key_cache;
     a.value_cache = s->value_cache;
-    a.query = s->step_operands;
-    a.new_key = s->step_operands + kQueryElems;
-    a.new_value = s->step_operands + kQueryElems + kRowElems;
-    a.out = s->attention;
     a.partition_tokens = 0;
     a.workspace = s->workspace;
     a.workspace_bytes = s->workspace_bytes;
+    const DecodeOperands32 f32{s->step_operands, s->step_operands + kQueryElems,
+                               s->step_operands + kQueryElems + kRowElems, s->attention};
     uint32_t launches = 0;
-    if (pvlc_hip_status st = launch_decode_checked(&a, rt->stream, &launches)) return st;
+    if (pvlc_hip_status st = launch_decode_checked(&a, rt->stream, &launches, &f32)) return st;
     rt->counters.kernel_launches += launches;
 
-    uint16_t *result = stage + kStepElems;
-    HIP_TRY(hipMemcpyAsync(result, s->attention, kQueryElems * 2, hipMemcpyDeviceToHost, rt->stream),
+    float *result = stage + kStepElems;
+    HIP_TRY(hipMemcpyAsync(result, s->attention, kQueryElems * 4, hipMemcpyDeviceToHost, rt->stream),
             "attention readback");
     rt->counters.device_to_host_copies += 1;
     const bool expire = s->expire_next_wait;
@@ -391,7 +406,10 @@ pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_oper
         s->fail_next_after_submit = false;
         return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE, "decoder KV session step: injected failure after submission");
     }
-    pvlc_hip_f16_to_f32_host(result, attention, kQueryElems);
+    std::memcpy(attention, result, kQueryElems * 4);
+    const size_t row = static_cast<size_t>(s->cache_tokens) * kRowElems;
+    std::memcpy(s->key_rows.data() + row, step->appended_key, kRowElems * 4);
+    std::memcpy(s->value_rows.data() + row, step->appended_value, kRowElems * 4);
     if (exec) {
         exec->cache_tokens_before = s->cache_tokens;
         exec->cache_tokens_after = s->cache_tokens + 1;
@@ -401,7 +419,11 @@ pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_oper
     return PVLC_HIP_OK;
 }
 
-// Copy the planes back to the compact f32 layout (rows 0..capacity-1).
+// Read the planes back and return the session's f32 rows (rows
+// 0..capacity-1, compact layout) once every device row is checked to hold
+// its f32 row rounded to fp16.  Rows the steps appended are finite and
+// rounded by the kernel; every other row (NaN tails included) was rounded by
+// f32_to_f16_rne at creation, so the comparison is bit for bit.
 pvlc_hip_status read_planes(pvlc_hip_kv_session *s, float *key_out, float *value_out) {
     pvlc_hip_runtime *rt = s->runtime;
     const size_t plane_elems = static_cast<size_t>(s->num_blocks) * kBlockTokens * kRowElems;
@@ -430,15 +452,22 @@ pvlc_hip_status read_planes(pvlc_hip_kv_session *s, float *key_out, float *value
         release.keep = wait_bounded(rt, false) != hipSuccess;
         return st;
     }
+    auto same = [](uint16_t device, float row) { return device == f32_to_f16_rne(row); };
     for (uint32_t t = 0; t < s->plan.cache_capacity; ++t) {
         for (uint32_t h = 0; h < kKvHeads; ++h) {
             for (uint32_t d = 0; d < kHeadDim; ++d) {
-                const size_t dst = (static_cast<size_t>(t) * kKvHeads + h) * kHeadDim + d;
-                key_out[dst] = f16_to_f32(kb[key_blocked_index(t, h, d)]);
-                value_out[dst] = f16_to_f32(vb[value_blocked_index(t, h, d)]);
+                const size_t src = (static_cast<size_t>(t) * kKvHeads + h) * kHeadDim + d;
+                if (!same(kb[key_blocked_index(t, h, d)], s->key_rows[src]) ||
+                    !same(vb[value_blocked_index(t, h, d)], s->value_rows[src]))
+                    return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE,
+                                "decoder KV session finish: the device cache differs from the session's rows at row " +
+                                    std::to_string(t));
             }
         }
     }
+    const size_t rows_elems = static_cast<size_t>(s->plan.cache_capacity) * kRowElems;
+    std::memcpy(key_out, s->key_rows.data(), rows_elems * 4);
+    std::memcpy(value_out, s->value_rows.data(), rows_elems * 4);
     return PVLC_HIP_OK;
 }
 

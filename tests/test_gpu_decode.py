@@ -57,7 +57,42 @@ def test_session_single_step_config1_shape(runtime):
     assert snap.cache_tokens == prefix + 1 and snap.cache_capacity == capacity
     np.testing.assert_array_equal(bits32(snap.key_cache[:(prefix + 1) * W]), bits32(ka))
     np.testing.assert_array_equal(bits32(snap.value_cache[:(prefix + 1) * W]), bits32(va))
-    assert np.all(np.isnan(snap.key_cache[(prefix + 1) * W:]))  # poison tail kept (as fp16 NaN)
+    # The poison tail comes back with its f32 payload.
+    assert np.all(bits32(snap.key_cache[(prefix + 1) * W:]) == bits32(POISON))
+    assert np.all(bits32(snap.value_cache[(prefix + 1) * W:]) == bits32(POISON))
+
+
+def rounded(x):
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("prefix,capacity", [(37, 45), (2047, 2060)])
+def test_session_finish_returns_f32_rows_as_given(runtime, prefix, capacity):
+    """Rows that fp16 does not hold exactly: finish returns every row bit for bit as it was given (the
+    descriptor's and each appended one), as the reference's f32 cache does; the attention is the decode of the
+    operands rounded to fp16 once (RNE), checked against the oracle on those rounded values."""
+    log(f"case: session f32 rows prefix={prefix} capacity={capacity}")
+    rng = np.random.default_rng(prefix)
+    keys = rng.standard_normal(capacity * W, dtype=np.float32)
+    values = rng.standard_normal(capacity * W, dtype=np.float32)
+    keys[prefix * W:] = POISON
+    values[prefix * W:] = POISON
+    assert np.any(rounded(keys[:prefix * W]) != keys[:prefix * W])
+    s = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(prefix, capacity, keys, values))
+    ka, va = keys[:prefix * W].copy(), values[:prefix * W].copy()
+    for i in range(3):
+        q = rng.standard_normal(2048, dtype=np.float32)
+        k = rng.standard_normal(W, dtype=np.float32)
+        v = rng.standard_normal(W, dtype=np.float32)
+        out = s.step(pvlc.DecoderKvSessionStep(q, k, v)).attention
+        ka, va = np.concatenate([ka, k]), np.concatenate([va, v])
+        t = prefix + 1 + i
+        check_close(out, O.decode_gqa_f32(rounded(q), rounded(ka), rounded(va), t, 16, 2, 128), f"step {i} T={t}")
+    snap = s.finish()
+    assert snap.cache_tokens == prefix + 3
+    np.testing.assert_array_equal(bits32(snap.key_cache[:(prefix + 3) * W]), bits32(ka))
+    np.testing.assert_array_equal(bits32(snap.value_cache[:(prefix + 3) * W]), bits32(va))
+    assert np.all(bits32(snap.key_cache[(prefix + 3) * W:]) == bits32(POISON))
 
 
 @pytest.mark.parametrize("prefix", [1, 2, 15, 16, 17, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 1023, 2047])
