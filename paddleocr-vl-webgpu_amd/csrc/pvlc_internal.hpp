@@ -185,17 +185,25 @@ int launch_linear_projection_f16(const float *input, const uint16_t *weight, con
 // of one kv head attends qb/4 + 1 steps of 64 keys, so a grid of one
 // workgroup per block is as long as its last block while most compute units
 // idle.  With a workspace, block l and block qblocks-1-l of a kv head (about
-// qblocks/4 + 2 steps together) go to two workgroups of equal length: the
-// first runs the light block, then the first k steps of the heavy one; the
-// second runs the rest of the heavy block (which holds the diagonal), and the
-// one that finishes last merges the two parts.  Used when the longest block
-// is longer than kPrefillSplitSteps.  A pair whose light workgroup would take
-// fewer than kPrefillSplitMin heavy steps is not split (the light block and
-// the heavy block run whole on the two workgroups): a second segment costs
-// its workgroup a query load, a pipeline fill and the partial hand-off, about
-// what 4 to 5 steps cost (measured at N=4096: 9-13 us for 1-2 steps).
+// qblocks/4 + 2 steps together) go to two workgroups of about equal time:
+// the first runs the light block, then the first k steps of the heavy one;
+// the second runs the rest of the heavy block (which holds the diagonal), and
+// the one that finishes last merges the two parts.  Used when the longest
+// block is longer than kPrefillSplitSteps.  A pair whose light workgroup
+// would take fewer than kPrefillSplitMin heavy steps at an even split is not
+// split (the light block and the heavy block run whole on the two
+// workgroups): a second segment costs its workgroup a query load, a pipeline
+// fill and the partial hand-off, about what 4 to 5 steps cost (measured at
+// N=4096: 9-13 us for 1-2 steps).  Of that, the light workgroup's extra
+// segment (the one the heavy workgroup does not run: query load, fill, last
+// steps and output stores of the light block) costs about 4 steps, so a
+// split pair moves kPrefillSplitShift heavy steps from the light workgroup to
+// the heavy one (config 4 at N=4096, shifts 0-3 on one box: 103.0-103.7,
+// 102.3, 100.0, 100.6-100.7 us mean per call).
 constexpr uint32_t kPrefillSplitSteps = 32;
 constexpr uint32_t kPrefillSplitMin = 5;
+constexpr uint32_t kPrefillSplitShift = 2;
+static_assert(kPrefillSplitMin > kPrefillSplitShift, "a split pair leaves the light workgroup a heavy step");
 constexpr uint32_t kPrefillPartialFloats = 4 * 64 * 74;  // 4 waves x 64 lanes x (2 x 9 x 4 O/l + 2 m)
 
 constexpr uint32_t prefill_block_steps(uint32_t qb) { return qb / 4 + 1; }
@@ -217,7 +225,8 @@ constexpr uint32_t prefill_pair_segments(uint32_t w, uint32_t qblocks, uint32_t 
     const uint32_t heavy = qblocks - 1u - *pair, light = *pair;
     const uint32_t sh = prefill_block_steps(heavy), sl = light == heavy ? 0u : prefill_block_steps(light);
     const uint32_t half = (sh - sl + 1u) / 2u;
-    const uint32_t k = half < kPrefillSplitMin ? 0u : half;  // heavy steps the light block's workgroup takes
+    // heavy steps the light block's workgroup takes (>= 3 when split)
+    const uint32_t k = half < kPrefillSplitMin ? 0u : half - kPrefillSplitShift;
     // Straight-line assignments (no runtime-indexed pointer), so that on the
     // device both segments stay in registers.  sh >= 1, so k >= sh implies k > 0.
     PrefillSegment s0{}, s1{};
