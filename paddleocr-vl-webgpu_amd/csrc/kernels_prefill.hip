@@ -594,8 +594,12 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
         // that arrives last merge the other one.  Partials move as 8-byte
         // relaxed agent-scope atomics (coherent across the XCDs' L2s); every
         // store of the workgroup completes before thread 0 counts the arrival.
-        // Slab of a part: O/l tiles [wave][ct][tile][half][lane] as float
-        // pairs, then m [wave][ct][lane].
+        // The second part first reads the count: when the first part has
+        // arrived (its workgroup runs it before its light block, so it
+        // usually has), its stores are complete, and the second part merges
+        // it without storing its own (the first part's count is then the
+        // last it touches).  Slab of a part: O/l tiles [wave][ct][tile][half]
+        // [lane] as float pairs, then m [wave][ct][lane].
         const uint32_t item = pair * kKvHeads + g;  // the heavy block of the pair
         auto slab = [&](uint32_t q) {
             return reinterpret_cast<uint64_t *>(p.partials + (static_cast<size_t>(item) * 2 + q) * kPrefillPartialFloats);
@@ -605,7 +609,15 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
             return p.partials + (static_cast<size_t>(item) * 2 + q) * kPrefillPartialFloats + 4 * 2 * 9 * 4 * 64 +
                    (wave * 2 + ct) * 64 + lane_e;
         };
-        {
+        bool merge_now = false;
+        if (part == 1) {
+            if (wave == 0 && lane_e == 0)
+                sm_last = __hip_atomic_load(p.counters + item, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;
+            __syncthreads();
+            merge_now = sm_last;  // uniform
+            __syncthreads();      // every wave has read it before it is written again below
+        }
+        if (!merge_now) {
             uint64_t *own = slab(part);
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
@@ -619,16 +631,16 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
                     }
                 __hip_atomic_store(m_ptr(part, ct), m_run[ct], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (wave == 0 && lane_e == 0) {
+                const uint32_t prev =
+                    __hip_atomic_fetch_add(p.counters + item, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                sm_last = prev == nparts - 1;
+            }
+            __syncthreads();
+            if (!sm_last) return;  // uniform: the other part merges and writes the block
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (wave == 0 && lane_e == 0) {
-            const uint32_t prev =
-                __hip_atomic_fetch_add(p.counters + item, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            sm_last = prev == nparts - 1;
-        }
-        __syncthreads();
-        if (!sm_last) return;  // uniform: the other part merges and writes the block
         const uint32_t q = part ^ 1u;  // two parts
         const uint64_t *other = slab(q);
 #pragma unroll
@@ -701,8 +713,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     // its first stages into these buffers.
     __syncthreads();
   };
-  // a light block, then part of a heavy one (two inlined copies: each is
-  // register-allocated like a single segment)
+  // the first part of a heavy block, then a light block (two inlined
+  // copies: each is register-allocated like a single segment)
   if (nseg > 0) run_segment(seg0);
   if (nseg > 1) run_segment(seg1);
 }

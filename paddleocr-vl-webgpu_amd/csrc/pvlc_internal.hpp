@@ -186,10 +186,13 @@ int launch_linear_projection_f16(const float *input, const uint16_t *weight, con
 // workgroup per block is as long as its last block while most compute units
 // idle.  With a workspace, block l and block qblocks-1-l of a kv head (about
 // qblocks/4 + 2 steps together) go to two workgroups of about equal time:
-// the first runs the light block, then the first k steps of the heavy one;
-// the second runs the rest of the heavy block (which holds the diagonal), and
-// the one that finishes last merges the two parts.  Used when the longest
-// block is longer than kPrefillSplitSteps.  A pair whose light workgroup
+// the first runs the first k steps of the heavy block, hands that part over,
+// then runs the light block; the second runs the rest of the heavy block
+// (which holds the diagonal) and merges the first part, which has arrived by
+// then (otherwise the part that arrives last merges).  Running the heavy part
+// first lets the second workgroup find it complete and merge it without
+// storing its own part: config 4 at N=4096, 99.8-100.8 -> 96.6-97.3 us mean
+// per call.  Used when the longest block is longer than kPrefillSplitSteps.  A pair whose light workgroup
 // would take fewer than kPrefillSplitMin heavy steps at an even split is not
 // split (the light block and the heavy block run whole on the two
 // workgroups): a second segment costs its workgroup a query load, a pipeline
@@ -198,8 +201,10 @@ int launch_linear_projection_f16(const float *input, const uint16_t *weight, con
 // segment (the one the heavy workgroup does not run: query load, fill, last
 // steps and output stores of the light block) costs about 4 steps, so a
 // split pair moves kPrefillSplitShift heavy steps from the light workgroup to
-// the heavy one (config 4 at N=4096, shifts 0-3 on one box: 103.0-103.7,
-// 102.3, 100.0, 100.6-100.7 us mean per call).
+// the heavy one (config 4 at N=4096, shifts 0-3 on one box with the light
+// block first: 103.0-103.7, 102.3, 100.0, 100.6-100.7 us mean per call; with
+// the heavy part first, shifts 1-4: 97.7-97.9, 96.6-97.3, 97.6-98.8,
+// 99.2-99.9).
 constexpr uint32_t kPrefillSplitSteps = 32;
 constexpr uint32_t kPrefillSplitMin = 5;
 constexpr uint32_t kPrefillSplitShift = 2;
@@ -234,12 +239,10 @@ constexpr uint32_t prefill_pair_segments(uint32_t w, uint32_t qblocks, uint32_t 
     if (role == 0) {
         const PrefillSegment hs = k >= sh ? PrefillSegment{heavy, 0u, 1u, 0u, sh} : PrefillSegment{heavy, 0u, 2u, 0u, k};
         if (sl) {
-            s0 = {light, 0u, 1u, 0u, sl};
-            n = 1;
-            if (k > 0) {
-                s1 = hs;
-                n = 2;
-            }
+            const PrefillSegment ls{light, 0u, 1u, 0u, sl};
+            s0 = k > 0 ? hs : ls;  // the heavy part first, then the light block
+            s1 = ls;
+            n = k > 0 ? 2u : 1u;
         } else if (k > 0) {
             s0 = hs;
             n = 1;
