@@ -976,7 +976,7 @@ def bench_token_chain(pvlc, torch, args):
             "eager_us_per_token": round(ms_eager * 1e3, 2),
             "attention_per_layer_us": round(ms_att * 1e3 / LAYERS, 3),
             "attention_18_layers_us": round(ms_att * 1e3, 2),
-            "attention_note": "18 single-layer decode launches (1 MB of keys and values each) replayed from a "
+            "attention_note": "18 single-layer decode launches (2 MB of keys and values each) replayed from a "
                               "graph back to back; config 2's headline runs the same 18 layers as one launch",
             "bytes_per_token": weight_bytes + att_bytes,
             "gbps": round((weight_bytes + att_bytes) / (ms_step * 1e-3) / 1e9, 1),
