@@ -515,8 +515,9 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     if (!sm_last) return;
 
     // Merge, per thread and without barriers: each thread loads the (max,
-    // sum) of its head and its elements of every partition, a batch of
-    // partitions at a time, and folds them into a running LSE combination.
+    // sum) of its head and its elements of every other partition, a batch of
+    // partitions at a time (its own are still in registers: reading them back
+    // cost config 2 ~0.2 us), and folds them into a running LSE combination.
     const float *all_o = p.part_o + unit * (kGroup * kHeadDim);
     const float *all_ml = p.part_ml + unit * (2 * kGroup);
     auto ld2 = [](const float *q, float *lo, float *hi) {
@@ -534,10 +535,17 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
 #pragma unroll
         for (int b = 0; b < kBatch; ++b) {
             const int q = min(q0 + b, num_parts - 1);  // clamped re-reads get weight 0 below
-            ld2(all_ml + q * (2 * kGroup) + 2 * h, &mv[b], &lv[b]);
+            if (q == static_cast<int>(part)) {  // uniform: this partition's own partial, still in registers
+                mv[b] = M;
+                lv[b] = L;
 #pragma unroll
-            for (int e = 0; e < kPer; e += 2)
-                ld2(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + e0 + e, &ov[b][e], &ov[b][e + 1]);
+                for (int e = 0; e < kPer; ++e) ov[b][e] = po[e];
+            } else {
+                ld2(all_ml + q * (2 * kGroup) + 2 * h, &mv[b], &lv[b]);
+#pragma unroll
+                for (int e = 0; e < kPer; e += 2)
+                    ld2(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + e0 + e, &ov[b][e], &ov[b][e + 1]);
+            }
         }
         float Mb = Mg;
 #pragma unroll
