@@ -370,23 +370,30 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
         // after the appended one (their weights are 0, but they may hold
         // poison and NaN * 0 would reach P.V); patch the appended token.
         if (ws + kChunkTokens > part_end || (ti >= 0 && ti < kChunkTiles)) {  // uniform
+            // The appended token's value at this lane's 8 dims, read from LDS
+            // by every lane whether it patches or not: with the reads inside
+            // the per-element condition the compiler branched around each of
+            // the 64 elements and waited for each read in turn (~2 us).
+            _Float16 nvv[8];
 #pragma unroll
-        for (int j = 0; j < PAIRS; ++j) {
-            const int tile = 2 * j + (kg >> 1);
-            const bool past = ws + tile * 16 >= part_end;
-            const bool append_here = tile == ti;
+            for (int c = 0; c < 8; ++c) nvv[c] = __builtin_bit_cast(_Float16, sm_new_v[c * 16 + row]);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int tok = (kg & 1) * 8 + e;
-                const bool zero = past || (append_here && tok > append_row);
-                const bool patch = append_here && tok == append_row;
+            for (int j = 0; j < PAIRS; ++j) {
+                const int tile = 2 * j + (kg >> 1);
+                const bool past = ws + tile * 16 >= part_end;
+                const bool append_here = tile == ti;
 #pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    const _Float16 v = patch ? __builtin_bit_cast(_Float16, sm_new_v[c * 16 + row]) : vr[j][c][e];
-                    vr[j][c][e] = zero ? static_cast<_Float16>(0.0f) : v;
+                for (int e = 0; e < 8; ++e) {
+                    const int tok = (kg & 1) * 8 + e;
+                    const bool zero = past || (append_here && tok > append_row);
+                    const bool patch = append_here && tok == append_row;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        const _Float16 v = patch ? nvv[c] : vr[j][c][e];
+                        vr[j][c][e] = zero ? static_cast<_Float16>(0.0f) : v;
+                    }
                 }
             }
-        }
         }
 
 #pragma unroll
