@@ -164,22 +164,28 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     const float *cos_row = rope ? p.rope_cos + static_cast<size_t>(pos) * 64 : nullptr;
     const float *sin_row = rope ? p.rope_sin + static_cast<size_t>(pos) * 64 : nullptr;
 
-    // Small operands are loaded first, unconditionally and before the
-    // key/value stream, so they return ahead of it and every later wait on
-    // them is a partial one.  The query is the B operand of the score MFMA:
-    // column = query head of the group (8 real, 8 zero), k = dims
-    // kb*32 + kg*8 .. +8 (lanes of the zero columns load a real row and
-    // discard it).
+    // Small operands are loaded first and before the key/value stream, so
+    // they return ahead of it and every later wait on them is a partial one.
+    // The query is the B operand of the score MFMA: column = query head of
+    // the group (8 real, 8 zero), k = dims kb*32 + kg*8 .. +8 (with fp16
+    // operands the lanes of the zero columns load a real row and discard it).
     // With f32 operands the query is kept as given until it is rotated, and
     // rounded to fp16 once (RNE), as the new key below.
     const size_t qoff = (static_cast<size_t>(s) * kQueryHeads + g * kGroup + (row & 7)) * kHeadDim;
     half8_t qb[4];
     float qf[F32IO ? 4 : 1][8];
     if constexpr (F32IO) {
+        // Only the lanes of the 8 real columns load the f32 query (8 KiB a
+        // wave otherwise, twice what the columns use: single-layer decode
+        // 7.98 -> 7.85 us; the fp16 query, half the bytes, stays unmasked,
+        // where masking measured 0.1 us slower on config 2).
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            const float4_t lo = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8);
-            const float4_t hi = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8 + 4);
+            float4_t lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
+            if (row < static_cast<int>(kGroup)) {
+                lo = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8);
+                hi = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8 + 4);
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 qf[kb][j] = lo[j];
@@ -628,6 +634,15 @@ __device__ inline int64_t checked_cache_len(const DecodeParams &p, int64_t len) 
 // ragged lengths when there are too many sequences for the ragged kernel.
 template <int WAVES, int PAIRS, bool F32IO>
 __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParams p) {
+    // Every argument the prologue reads, loaded in one round of scalar loads:
+    // left to itself the compiler loads them where each is first needed, and
+    // the branches on the optional pointers made that four dependent rounds
+    // before the first key/value load (config 2: 11.91-11.94 -> 11.70-11.75 us).
+    asm volatile("" ::"s"(p.cache_lens), "s"(p.uniform_cache_len), "s"(p.block_tables), "s"(p.max_blocks_per_seq),
+                 "s"(p.num_blocks), "s"(p.partition_tokens), "s"(p.max_parts), "s"(p.positions), "s"(p.key_cache),
+                 "s"(p.value_cache), "s"(p.rope_cos), "s"(p.rope_sin), "s"(p.rope_rows));
+    if constexpr (F32IO) asm volatile("" ::"s"(p.query32), "s"(p.new_key32), "s"(p.new_value32));
+    else asm volatile("" ::"s"(p.query), "s"(p.new_key), "s"(p.new_value));
     const uint32_t part = blockIdx.x;
     const uint32_t g = blockIdx.y;  // kv head
     const uint32_t s = blockIdx.z;  // sequence (or layer)
