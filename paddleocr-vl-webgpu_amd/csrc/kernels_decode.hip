@@ -511,6 +511,9 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     constexpr bool kWide = kPer % 4 == 0;
     constexpr int kSc1 = 16;  // cache-policy operand of the buffer intrinsics: sc1
     typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    // Raw buffer over this unit's partials: stride 0, 2^31 - 1 bytes, and the
+    // fourth descriptor word of a raw 32-bit-element buffer on gfx9-family
+    // parts (data format 32 in bits 15-18).
     const __amdgpu_buffer_rsrc_t o_rsrc =
         __builtin_amdgcn_make_buffer_rsrc(p.part_o + unit * (kGroup * kHeadDim), 0, 0x7fffffff, 0x00020000);
     auto pack = [](float lo, float hi) {
