@@ -139,8 +139,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_f16_kernel(const uint16_
 #pragma unroll
             for (int j = 0; j < 8; ++j)
                 acc = __builtin_fmaf(static_cast<float>(w[r][c][j]), x[c][j >> 2][j & 3], acc);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+        acc = wave_sum(acc);
         if (row0 + r < rows) {
             if (out != nullptr && lane == 0) out[row0 + r] = acc;
             if constexpr (TOP1) {
@@ -175,6 +174,10 @@ template <int CHUNKS>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_group_f16_kernel(GemvGroup g,
                                                                            const float *__restrict__ vector) {
     constexpr int kColumns = CHUNKS * 512;
+    // The output pointers are read only by the storing lane at the end; named
+    // here, they arrive with the other arguments instead of in a scalar-load
+    // round trip of their own after the reduction.
+    asm volatile("" ::"s"(g.out[0]), "s"(g.out[1]), "s"(g.out[2]), "s"(g.out[3]));
     const int lane = threadIdx.x & 63;
     const uint32_t grow =
         static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * kGemvWaves + (threadIdx.x >> 6))));
@@ -203,8 +206,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_group_f16_kernel(GemvGro
     for (int c = 0; c < CHUNKS; ++c)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(static_cast<float>(w[c][j]), x[c][j >> 2][j & 3], acc);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    acc = wave_sum(acc);
     if (grow < g.total && lane == 0) store_f32(obase, row, acc);
 }
 

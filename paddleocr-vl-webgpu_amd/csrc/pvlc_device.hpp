@@ -89,4 +89,28 @@ __device__ inline half8_t round_chunk(const float *src) {
     return r;
 }
 
+// A DPP move of a float within the rows of 16 lanes (CTRL: the dpp_ctrl
+// encoding, all rows and banks enabled).
+template <int CTRL>
+__device__ inline float dpp_f32(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wave, returned in every lane (a wave-uniform
+// value).  DPP moves within each 16-lane row (xor 1 and xor 2 inside quads,
+// then rotations by 4 and 8: every lane holds its row's sum), then the four
+// row sums read from lanes 0, 16, 32 and 48.  A butterfly of __shfl_xor
+// compiles to six dependent LDS permutes instead.
+__device__ inline float wave_sum(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x124>(v);  // row_ror:4
+    v += dpp_f32<0x128>(v);  // row_ror:8
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 }  // namespace pvlc
