@@ -8,8 +8,9 @@
 //
 // A batch-1 GEMV streams the weights once, so it is HBM-bound: each wave owns
 // RPW rows and reads them in 16-byte lanes (a wave-wide load is one 1 KiB
-// contiguous run of a row); the vector stays in registers (lane l holds the 8
-// columns of each of its 16-byte chunks); every row load of the wave is
+// contiguous run of a row); the vector, loaded once per workgroup through
+// LDS, stays in registers (lane l holds the 8 columns of each of its 16-byte
+// chunks); every row load of the wave is
 // issued before the first dot product; one cross-lane reduction per row.
 //
 // Top-1 candidates are packed into one u64 whose unsigned order is the
@@ -103,6 +104,39 @@ __global__ __launch_bounds__(64) void top1_finish_kernel(Top1Slot *slots, uint32
 }
 
 // CHUNKS = columns / 512: 16-byte chunks of a row per lane.
+
+// The vector, loaded once per workgroup: thread t loads float4 chunks t,
+// t + 256, ... into LDS, and after one barrier every lane reads the 8
+// columns (c * 64 + lane) * 8 .. +8 of each chunk c it multiplies.  Each
+// wave loading the whole vector itself put four times its bytes through the
+// compute unit's load path next to the weights (decoder GEMV step replayed:
+// 262.4 -> 253.8 us).  The 2048-column shape (o) measured 0.1 us slower this
+// way and keeps the per-wave loads.
+template <int CHUNKS>
+__device__ inline void load_vector_lds(const float *__restrict__ vector, float4_t (&x)[CHUNKS][2]) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (CHUNKS == 4) {
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            x[c][0] = *reinterpret_cast<const float4_t *>(vector + (c * 64 + lane) * 8);
+            x[c][1] = *reinterpret_cast<const float4_t *>(vector + (c * 64 + lane) * 8 + 4);
+        }
+    } else {
+        constexpr int kQuads = CHUNKS * 512 / 4;  // float4 chunks of the vector
+        __shared__ float4_t sv[kQuads];
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < kQuads / (kGemvWaves * 64); ++i)
+            sv[t + i * kGemvWaves * 64] = reinterpret_cast<const float4_t *>(vector)[t + i * kGemvWaves * 64];
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < CHUNKS; ++c) {
+            x[c][0] = sv[(c * 64 + lane) * 2];
+            x[c][1] = sv[(c * 64 + lane) * 2 + 1];
+        }
+    }
+}
+
 template <int CHUNKS, int RPW, bool TOP1>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_f16_kernel(const uint16_t *__restrict__ weights,
                                                                      const float *__restrict__ vector,
@@ -123,11 +157,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_f16_kernel(const uint16_
             w[r][c] = __builtin_nontemporal_load(reinterpret_cast<const half8_t *>(wr + (c * 64 + lane) * 8));
     }
     float4_t x[CHUNKS][2];
-#pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-        x[c][0] = *reinterpret_cast<const float4_t *>(vector + (c * 64 + lane) * 8);
-        x[c][1] = *reinterpret_cast<const float4_t *>(vector + (c * 64 + lane) * 8 + 4);
-    }
+    load_vector_lds<CHUNKS>(vector, x);
     __shared__ Top1Lds lds;
     if constexpr (TOP1) top1_lds_init(lds);  // while the loads are in flight
     uint64_t best = 0;  // below every candidate (the low word ~index is nonzero)
@@ -196,11 +226,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_group_f16_kernel(GemvGro
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c) w[c] = load_half8_nt(wbase, static_cast<size_t>(row) * kColumns + (c * 64 + lane) * 8);
     float4_t x[CHUNKS][2];
-#pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-        x[c][0] = *reinterpret_cast<const float4_t *>(vector + (c * 64 + lane) * 8);
-        x[c][1] = *reinterpret_cast<const float4_t *>(vector + (c * 64 + lane) * 8 + 4);
-    }
+    load_vector_lds<CHUNKS>(vector, x);
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c)
