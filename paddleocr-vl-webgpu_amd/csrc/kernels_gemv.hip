@@ -123,6 +123,7 @@ __device__ inline void load_vector_lds(const float *__restrict__ vector, float4_
         }
     } else {
         constexpr int kQuads = CHUNKS * 512 / 4;  // float4 chunks of the vector
+        static_assert(kQuads % (kGemvWaves * 64) == 0, "every thread loads the same number of chunks");
         __shared__ float4_t sv[kQuads];
         const int t = threadIdx.x;
 #pragma unroll
