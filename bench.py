@@ -822,7 +822,8 @@ class TokenChain:
     f32_operands=False runs the fp16 entry point pvlc_hip_paged_decode_f16 instead, with a torch conversion of
     q|k|v to fp16 before it and of its fp16 output to f32 after it (two more launches per layer)."""
 
-    def __init__(self, pvlc, torch, layers, context, capacity, head_rows, seed=21, f32_operands=True):
+    def __init__(self, pvlc, torch, layers, context, capacity, head_rows, seed=21, f32_operands=True,
+                 partition_tokens=0):
         dev = torch.device("cuda:0")
         gen = torch.Generator(device=dev).manual_seed(seed)
         self.pvlc, self.torch, self.layers, self.context, self.head_rows = pvlc, torch, layers, context, head_rows
@@ -854,7 +855,7 @@ class TokenChain:
         pvlc.workspace_init(self.tws, self.tws_bytes)
         cos, sin = pvlc.rope_table(ROPE_BASE, capacity)
         self.cos, self.sin = torch.from_numpy(cos.ravel()).to(dev), torch.from_numpy(sin.ravel()).to(dev)
-        self.wsb = pvlc.decode_workspace_bytes(1, capacity)
+        self.wsb = pvlc.decode_workspace_bytes(1, capacity, partition_tokens)
         self.ws = torch.empty(self.wsb, dtype=torch.uint8, device=dev)
         pvlc.workspace_init(self.ws, self.wsb)
         self.qkv_members, self.gu_members, self.decode_args = [], [], []
@@ -874,7 +875,7 @@ class TokenChain:
                 new_key=q16[2048:2304] if fp16 else None, new_value=q16[2304:] if fp16 else None,
                 out=self.attn16[l] if fp16 else None, workspace=self.ws, workspace_bytes=self.wsb,
                 max_context=capacity, uniform_cache_len=context - 1, rope_cos=self.cos, rope_sin=self.sin,
-                rope_rows=capacity, rotate_query=True))
+                rope_rows=capacity, rotate_query=True, partition_tokens=partition_tokens))
         torch.cuda.synchronize()
 
     def attention(self, l, st):
@@ -938,7 +939,8 @@ def _measure_chain(pvlc, torch, args, f32_operands):
     """One TokenChain: the step replayed from a HIP graph (the first replay checked bit for bit against the eager
     step), its attention launches alone, and the step launched eagerly."""
     stream = torch.cuda.current_stream()
-    chain = TokenChain(pvlc, torch, LAYERS, CONTEXT, CAPACITY, GEMV_HEAD[1], f32_operands=f32_operands)
+    chain = TokenChain(pvlc, torch, LAYERS, CONTEXT, CAPACITY, GEMV_HEAD[1], f32_operands=f32_operands,
+                       partition_tokens=args.partition)
     chain.step(stream)
     torch.cuda.synchronize()
     eager = chain.state()
@@ -972,6 +974,7 @@ def bench_token_chain(pvlc, torch, args):
                         "LM head 103424x1024 fused with greedy top-1; norms and SwiGLU left out (outside this "
                         "backend)",
             "launches_per_step": LAYERS * 5 + 2,
+            "decode_partition_tokens": args.partition or "automatic",
             "graph_us_per_token": round(ms_step * 1e3, 2), "graph_spread": stats,
             "eager_us_per_token": round(ms_eager * 1e3, 2),
             "attention_per_layer_us": round(ms_att * 1e3 / LAYERS, 3),
