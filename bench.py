@@ -61,8 +61,6 @@ def parse():
                     help="bound of each CPU baseline sample of configs 3, 4 and 5 in the default run")
     ap.add_argument("--only-config2", action="store_true",
                     help="default run without the configs 3, 4 and 5 legs")
-    ap.add_argument("--read-floor", action="store_true",
-                    help="HBM read probe: one launch streaming the config-2 step's bytes with several grids")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=0,
                     help="only run this many steps (no CPU leg), for rocprofv3 runs")
@@ -88,8 +86,6 @@ def main() -> int:
         return 2
     if args.calibrate_copy:
         return calibrate_copy(args)
-    if args.read_floor:
-        return bench_read_floor(args)
     if args.gemv:
         return bench_gemv(args)
     if args.projection:
@@ -291,59 +287,6 @@ def measure_config2(pvlc, torch, args):
     result["inputs"] = {"generator": "numpy PCG64 standard_normal -> f32 -> fp16 (replica 0, the CPU baseline inputs), torch Philox randn on the device (replicas 1..)", "seeds": {"numpy": 2048, "torch": 7}, "note": "not the splitmix64/Box-Muller streams of the survey; timings do not depend on the N(0,1) generator"}
     del replicas, sweep
     return result
-
-
-# Read-probe shapes (workgroups, waves, KiB per wave): the config-2 decode grid as launched (216 workgroups of 12
-# waves, 16 KiB each: the 37.75 MiB of keys and values plus the re-reads of short last partitions), then
-# 37.75 MiB exactly under other grids.
-READ_FLOOR_SHAPES = ((252, 10, 16), (216, 12, 16), (288, 8, 16), (144, 16, 16), (576, 4, 16), (1152, 4, 8), (144, 8, 32),
-                     (256, 12, 8), (512, 12, 8))
-
-
-def bench_read_floor(args):
-    """One launch of a pure HBM read (paddleocr-vl-webgpu_amd/probes/hbm_read.hip) per shape: the time a launch
-    needs to stream the config-2 step's bytes with no compute and no merge, on cache-cold data (the windows rotate
-    through 600 MiB, beyond the 256 MiB Infinity Cache).  Mean of back-to-back launches and per-launch
-    percentiles, as for the decode step."""
-    import ctypes
-
-    import torch
-
-    from __graft_entry__ import load_package
-
-    load_package()  # torch first, then the HIP libraries: one HIP runtime in the process
-    probe = ctypes.CDLL(os.path.join(REPO, "paddleocr-vl-webgpu_amd", "libpvlc_probes.so"))
-    probe.pvlc_probe_hbm_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
-                                          ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
-    probe.pvlc_probe_hbm_read.restype = ctypes.c_int
-    stream = torch.cuda.current_stream()
-    pool = torch.randint(0, 2**31 - 1, ((600 << 20) // 4,), dtype=torch.int32, device="cuda")
-    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
-    rows = []
-    for wgs, waves, kib in READ_FLOOR_SHAPES:
-        nbytes = wgs * waves * kib * 1024
-        windows = pool.numel() * 4 // nbytes
-
-        def launch(i, wgs=wgs, waves=waves, kib=kib, nbytes=nbytes, windows=windows):
-            src = pool.data_ptr() + (i % windows) * nbytes
-            e = probe.pvlc_probe_hbm_read(src, sink.data_ptr(), wgs, waves, kib, 0x9E3779B9, stream.cuda_stream)
-            assert e == 0, f"probe launch failed: {e}"
-
-        for i in range(args.warmup):
-            launch(i)
-        ms = _timed_launches(torch, stream, args.steps, launch)
-        stats = _launch_stats(torch, stream, args.steps, launch)
-        rows.append({"workgroups": wgs, "waves": waves, "kib_per_wave": kib, "bytes": nbytes,
-                     "us": round(ms * 1e3, 3), "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                     "pct_hbm_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
-                     "launch_stats": stats})
-    step_bytes = LAYERS * algorithmic_bytes(CONTEXT)
-    best = min(rows, key=lambda r: r["us"] * step_bytes / r["bytes"])
-    print(json.dumps({"metric": "HBM read floor for the config-2 step's bytes (one launch, no compute)",
-                      "shapes": rows, "config2_step_bytes": step_bytes,
-                      "best_scaled_to_step_us": round(best["us"] * step_bytes / best["bytes"], 3),
-                      "steps": args.steps, "warmup": args.warmup}, ensure_ascii=False))
-    return 0
 
 
 def calibrate_copy(args):

@@ -19,9 +19,6 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 INCLUDE = os.path.join(REPO, "include")
 LIB = os.path.join(HERE, "libpvlc_hip.so")
-# Measurement probes (not part of the backend's ABI), loaded by bench.py only.
-PROBES = os.path.join(HERE, "probes")
-PROBE_LIB = os.path.join(HERE, "libpvlc_probes.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -69,15 +66,6 @@ def build(verbose: bool = False) -> str:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, LIB)
-    probe_srcs = sorted(glob.glob(os.path.join(PROBES, "*.hip")))
-    if probe_srcs:
-        probe_objs = [_compile(src) for src in probe_srcs]
-        tmp = PROBE_LIB + ".tmp"
-        proc = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *probe_objs],
-                              capture_output=True, text=True)
-        if proc.returncode != 0:
-            raise RuntimeError(f"probe link failed:\n{proc.stdout}\n{proc.stderr}")
-        os.replace(tmp, PROBE_LIB)
     if verbose:
         print(f"built {LIB}")
     return LIB
