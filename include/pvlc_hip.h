@@ -436,10 +436,13 @@ pvlc_hip_status pvlc_hip_paged_decode_f32io(const pvlc_hip_paged_decode_args *ar
  * pvlc_hip_workspace_error.  At most 4096 sequences; a launch whose split-K
  * state exceeds 16 MiB is rejected (InvalidDecoderGeometry) -- configs with
  * up to 64 sequences of 8192 rows fit.  The first call on a device looks up
- * the array's address there, clears its counters and waits for that clear on
- * `stream` once; later calls never synchronise.  Every call on one device
- * shares that device's array and leaves it ready for the next call: calls
- * that overlap on one device (two streams, two threads) race. */
+ * the array's address there (hipGetSymbolAddress); no call launches anything
+ * but the decode kernels or synchronises, so any call, the first included,
+ * may be captured into a HIP graph.  Every call on one device shares that
+ * device's array and leaves it ready for the next call (the merge counters
+ * start at zero and count whole generations per launch): calls that overlap
+ * on one device (two streams, two threads, a graph replay beside a direct
+ * call) race and garble their outputs; later calls are unaffected. */
 pvlc_hip_status pvlc_hip_paged_decode_f16_no_alloc(const pvlc_hip_paged_decode_args *args, uint32_t *error_word,
                                                    void *stream);
 

@@ -27,10 +27,16 @@ using namespace pvlc;
 // context fit; larger launches are rejected and use a workspace.
 constexpr size_t kScratchBytes = size_t{16} << 20;
 // Sequences (or layers) one call admits.  The merge counters sit at a fixed
-// place for every call, so a call always finds them zero: they are zeroed
-// once per device at set-up and every launch leaves them zero.
+// place for every call.  They start at zero (the array is static storage,
+// zero when the code object is loaded) and count arrivals in generations
+// (kArrivalSpan): every completed launch leaves each counter a multiple of
+// the span, which is all the next launch needs, so nothing is cleared here.
+// Calls that overlap on one device garble their own outputs, but once both
+// have completed the counters are consistent again.
 constexpr uint32_t kMaxSeqs = 4096;
 constexpr size_t kStatusOffset = 0;  // [unused error word][automatic partition][compute units], 256-byte slot
+// (the two status words are written by the streaming kernel before its merge
+// kernel reads them, so they need no initial value)
 constexpr size_t kCountersOffset = 256;
 constexpr size_t kPartialsOffset = kCountersOffset + size_t{kMaxSeqs} * kKvHeads * sizeof(uint32_t);
 static_assert(kPartialsOffset % 256 == 0, "partials start on a 256-byte line");
@@ -47,10 +53,10 @@ std::mutex g_mu;
 void *g_scratch[kMaxDevices] = {};
 
 // Set-up on the current device (first call there): the array's address on
-// this device, then the status slot and the counters zeroed with a fill
-// kernel on the caller's stream, waited for so that calls on any stream
-// find them zero.
-pvlc_hip_status device_scratch(void *stream, char **out) {
+// this device.  Nothing is launched or waited for, so a first call made
+// while the caller's stream is being captured into a graph is captured like
+// any other.
+pvlc_hip_status device_scratch(char **out) {
     int device = 0;
     if (hipError_t e = hipGetDevice(&device))
         return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE, std::string("hipGetDevice: ") + hipGetErrorString(e));
@@ -63,12 +69,6 @@ pvlc_hip_status device_scratch(void *stream, char **out) {
             return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE,
                         std::string("decode scratch address: ") + hipGetErrorString(e));
         if (!ptr) return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE, "decode scratch address is NULL");
-        if (int e = launch_fill_u32(static_cast<uint32_t *>(ptr), kPartialsOffset / 4, 0u, stream))
-            return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE,
-                        std::string("decode scratch clear: ") + hipGetErrorString(static_cast<hipError_t>(e)));
-        if (hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream)))
-            return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE,
-                        std::string("decode scratch clear: ") + hipGetErrorString(e));
         g_scratch[device] = ptr;
     }
     *out = static_cast<char *>(g_scratch[device]);
@@ -102,7 +102,7 @@ extern "C" pvlc_hip_status pvlc_hip_paged_decode_f16_no_alloc(const pvlc_hip_pag
                            " bytes of scratch pvlc_hip_paged_decode_f16_no_alloc holds per device; use "
                            "pvlc_hip_paged_decode_f16 with a workspace");
     char *base = nullptr;
-    if (pvlc_hip_status st = device_scratch(stream, &base)) return st;
+    if (pvlc_hip_status st = device_scratch(&base)) return st;
     const DecodeState state{reinterpret_cast<float *>(base + o_offset),
                             reinterpret_cast<float *>(base + ml_offset),
                             reinterpret_cast<uint32_t *>(base + kCountersOffset),

@@ -8,11 +8,12 @@
 // 1 KiB (keys) or 512 B (values) run -- and serves all 8 query heads of the
 // group with matrix instructions:
 //   scores  S[token][head] = K[token][:] . Q[head][:]   v_mfma_f32_16x16x32_f16
-//   output  O[head][dim]  += P[head][token] V[token][dim] v_mfma_f32_16x16x16_f16
-// The QK accumulator layout (lane holds 4 consecutive tokens of one head) is
-// exactly the PV A-operand layout, so probabilities never leave the lane.
-// Softmax statistics use cross-lane shuffles; waves combine through LDS; the
-// last partition to finish (device-scope counter) merges all partitions.
+//   output  O[head][dim]  += P[head][token] V[token][dim] v_mfma_f32_16x16x32_f16
+// The two score MFMAs of a tile pair leave each lane 8 consecutive tokens of
+// one head: exactly the PV A-operand layout, so probabilities never leave the
+// lane.  Softmax statistics use cross-lane shuffles; waves combine through
+// LDS; the partitions of a (sequence, kv head) count their arrivals on a
+// device-scope counter, and the last to arrive merges all partitions.
 //
 // Latency discipline (the whole step is a few microseconds): every wave
 // issues its first chunk's loads before anything else; block ids come from
@@ -131,15 +132,25 @@ __device__ inline void load_chunk(const DecodeParams &p, uint32_t g, uint32_t id
                 reinterpret_cast<const half8_t *>(vbase[j] + (cc * 16 + row) * 16 + (kg & 1) * 8));
 }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kSc1 = 16;  // cache-policy operand of the buffer intrinsics: sc1 (agent scope)
+
+// An 8-byte agent-scope (sc1) load of two floats.
+__device__ inline void load_pair_sc1(const float *q, float *lo, float *hi) {
+    const uint64_t v =
+        __hip_atomic_load(reinterpret_cast<const uint64_t *>(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *lo = __uint_as_float(static_cast<uint32_t>(v));
+    *hi = __uint_as_float(static_cast<uint32_t>(v >> 32));
+}
+
 // One work item: partition `part` of kv head g of sequence s, whose cache
 // holds cache_len rows before the append (rotary position pos); ids are the
 // wave's tile block ids (wave_tile_ids) and ids_bad whether one of them was
 // out of range.  With DEFER_MERGE the partial is only stored (plain stores)
 // for paged_decode_merge_kernel, launched after this kernel; otherwise the
-// last partition to finish merges in-kernel.  Every return is uniform over
-// the workgroup.  Errors are
-// reported after the key/value loads are consumed, so no conditional memory
-// operation sits among them.
+// last partition to arrive merges all partitions in-kernel.  Every return is
+// uniform over the workgroup.  Errors are reported after the key/value loads
+// are consumed, so no conditional memory operation sits among them.
 template <int WAVES, int PAIRS, bool DEFER_MERGE, bool F32IO>
 __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uint32_t g, uint32_t part, int cache_len,
                                    int pos, uint32_t ids, bool ids_bad) {
@@ -402,17 +413,33 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
             }
         }
 
+        // P.V with P in fp16: the weights of the fp16 entry points.  The f32
+        // entry points carry each weight as an exact-in-f32 pair hi + lo of
+        // fp16 values (hi = fp16(p), lo = fp16(p - hi)), so P.V takes two
+        // MFMAs and the weights keep ~22 bits instead of 11 (the fp16 P is the
+        // dominant error of the output against the f32 reference: rel-L2
+        // ~2e-4 with it, ~1e-6 with the pair).
 #pragma unroll
         for (int j = 0; j < PAIRS; ++j) {
-            half8_t pa;
+            half8_t pa, pl;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const _Float16 ph = to_h(__builtin_amdgcn_exp2f(x[j][e] - m_new));
+                const float pf = __builtin_amdgcn_exp2f(x[j][e] - m_new);
+                const _Float16 ph = to_h(pf);
                 pa[e] = ph;
-                l_run += static_cast<float>(ph);  // the weights P.V actually uses
+                if constexpr (F32IO) {
+                    const _Float16 plo = to_h(pf - static_cast<float>(ph));  // pf - ph is exact in f32
+                    pl[e] = plo;
+                    l_run += static_cast<float>(ph) + static_cast<float>(plo);  // the weights P.V uses
+                } else {
+                    l_run += static_cast<float>(ph);  // the weights P.V actually uses
+                }
             }
 #pragma unroll
-            for (int c = 0; c < 8; ++c) o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vr[j][c], o[c], 0, 0, 0);
+            for (int c = 0; c < 8; ++c) {
+                o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vr[j][c], o[c], 0, 0, 0);
+                if constexpr (F32IO) o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vr[j][c], o[c], 0, 0, 0);
+            }
         }
     }
     l_run += __shfl_xor(l_run, 16);
@@ -443,7 +470,8 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     // Each of the first kCT threads (a power of two) owns kPer consecutive
     // output elements of one head; the others shadow thread 0 and store
     // nothing.
-    constexpr int kCT = kThreads >= 1024 ? 1024 : (kThreads >= 512 ? 512 : (kThreads >= 256 ? 256 : 128));
+    constexpr int kCT =
+        kThreads >= 1024 ? 1024 : (kThreads >= 512 ? 512 : (kThreads >= 256 ? 256 : (kThreads >= 128 ? 128 : 64)));
     constexpr int kPer = (kGroup * kHeadDim) / kCT;
     const bool active = threadIdx.x < kCT;
     const int e0 = active ? static_cast<int>(threadIdx.x) * kPer : 0;
@@ -509,8 +537,6 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     // single-layer decode 8.48 -> 8.17 us.
     static_assert(kPer % 2 == 0, "partials move as float pairs");
     constexpr bool kWide = kPer % 4 == 0;
-    constexpr int kSc1 = 16;  // cache-policy operand of the buffer intrinsics: sc1
-    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
     // Raw buffer over this unit's partials: stride 0, 2^31 - 1 bytes, and the
     // fourth descriptor word of a raw 32-bit-element buffer on gfx9-family
     // parts (data format 32 in bits 15-18).
@@ -542,31 +568,33 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     // workgroup's __syncthreads() emits no wait), then for every wave.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    // Arrival, counted in generations (kArrivalSpan): the partition with the
+    // highest index adds kArrivalSpan - (num_parts - 1), the others 1, so the
+    // arrival that completes a multiple of kArrivalSpan is the last one, and
+    // the counter is left ready for the next launch without a reset.
     if (threadIdx.x == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(p.counters + s * kKvHeads + g, 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        sm_last = (prev == static_cast<uint32_t>(num_parts - 1));
+        const uint32_t inc =
+            part == static_cast<uint32_t>(num_parts - 1) ? kArrivalSpan - static_cast<uint32_t>(num_parts - 1) : 1u;
+        const uint32_t prev =
+            __hip_atomic_fetch_add(p.counters + s * kKvHeads + g, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sm_last = ((prev + inc) & (kArrivalSpan - 1)) == 0;
     }
     __syncthreads();
     if (!sm_last) return;
+
+    const float *all_ml = p.part_ml + unit * (2 * kGroup);
 
     // Merge, per thread and without barriers: each thread loads the (max,
     // sum) of its head and its elements of every other partition, a batch of
     // partitions at a time (its own are still in registers: reading them back
     // cost config 2 ~0.2 us), and folds them into a running LSE combination.
     const float *all_o = p.part_o + unit * (kGroup * kHeadDim);
-    const float *all_ml = p.part_ml + unit * (2 * kGroup);
-    auto ld2 = [](const float *q, float *lo, float *hi) {
-        const uint64_t v =
-            __hip_atomic_load(reinterpret_cast<const uint64_t *>(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *lo = __uint_as_float(static_cast<uint32_t>(v));
-        *hi = __uint_as_float(static_cast<uint32_t>(v >> 32));
-    };
     // The wide shapes take 16 partitions per batch (one round of loads for
-    // the single-sequence decode's 16: 8.17 -> 7.87 us) and load only the
+    // the single-sequence decode's 16: 8.17 -> 7.87 us; 4 with the 16
+    // elements a thread of the one-wave shape owns) and load only the
     // partitions that exist; the others keep batches of 8 with clamped
     // re-reads.
-    constexpr int kBatch = kWide ? 16 : 8;
+    constexpr int kBatch = kPer >= 16 ? 4 : (kWide ? 16 : 8);
     float Mg = -INFINITY, Lg = 0.f, og[kPer];
 #pragma unroll
     for (int e = 0; e < kPer; ++e) og[e] = 0.f;
@@ -583,7 +611,7 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
 #pragma unroll
                 for (int e = 0; e < kPer; ++e) ov[b][e] = po[e];
             } else {
-                ld2(all_ml + q * (2 * kGroup) + 2 * h, &mv[b], &lv[b]);
+                load_pair_sc1(all_ml + q * (2 * kGroup) + 2 * h, &mv[b], &lv[b]);
                 if constexpr (kWide) {
 #pragma unroll
                     for (int e = 0; e < kPer; e += 4) {
@@ -595,7 +623,8 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
                 } else {
 #pragma unroll
                     for (int e = 0; e < kPer; e += 2)
-                        ld2(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + e0 + e, &ov[b][e], &ov[b][e + 1]);
+                        load_pair_sc1(all_o + static_cast<size_t>(q) * (kGroup * kHeadDim) + e0 + e, &ov[b][e],
+                                      &ov[b][e + 1]);
                 }
             }
         }
@@ -621,8 +650,6 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
 #pragma unroll
         for (int e = 0; e < kPer; ++e) put(e0 + e, og[e] * inv);
     }
-    if (threadIdx.x == 0)
-        __hip_atomic_store(p.counters + s * kKvHeads + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Cache length of sequence s if it is valid for this launch (one row to
@@ -961,11 +988,12 @@ int launch_paged_decode_kernels(const DecodeLaunch &launch, DecodeParams &p, hip
     }
 
     // Single-shot regime: one workgroup per (partition, kv head, sequence);
-    // the last partition to finish merges.
+    // the last partition to arrive merges.
     const dim3 grid(launch.max_parts, kKvHeads, a.num_seqs);
 #define PVLC_DECODE_LAUNCH(W, PR) \
     hipLaunchKernelGGL((paged_decode_kernel<W, PR, F32IO>), grid, dim3((W) * 64), 0, st, p)
     switch (launch.waves) {
+        case 1: PVLC_DECODE_LAUNCH(1, 1); break;
         case 2: PVLC_DECODE_LAUNCH(2, 1); break;
         case 4: PVLC_DECODE_LAUNCH(4, 1); break;
         case 6: PVLC_DECODE_LAUNCH(6, 1); break;

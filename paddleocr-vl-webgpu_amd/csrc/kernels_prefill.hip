@@ -479,6 +479,38 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
         for (int ct = 0; ct < 2; ++ct) o[ct][8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[ct][j], ones, o[ct][8], 0, 0, 0);
     };
 
+    // The f32 entry point's weights and P.V for pair j: each weight p as the
+    // pair hi = fp16(p), lo = fp16(p - hi) (p - hi is exact in f32), so the
+    // weights keep ~22 bits instead of 11; P.V and the row sums take hi, then
+    // lo, over one read of the value fragments.
+    auto pv_mfma_hi_lo = [&](const uint16_t *vl, int j, const Scores &x, const float (&ms)[2]) {
+        half8_t hi[2], lo[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float pf = __builtin_amdgcn_exp2f(__builtin_fmaf(x[ct][j][e], scale, -ms[ct]));
+                hi[ct][e] = to_h(pf);
+                lo[ct][e] = to_h(pf - static_cast<float>(hi[ct][e]));
+            }
+        half8_t vf[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            vf[c] = *reinterpret_cast<const half8_t *>(vl + lds_value_offset(j, kg >> 1, kg & 1, c * 16 + row));
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+                    o[ct][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pass ? lo[ct] : hi[ct], vf[c], o[ct][c], 0, 0, 0);
+            }
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+                o[ct][8] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pass ? lo[ct] : hi[ct], ones, o[ct][8], 0, 0, 0);
+        }
+    };
+
     // Software pipeline: while the score MFMAs of step i+1 run, the VALU
     // exponentiates step i (and rescales O when the reference moved); while
     // P.V of step i runs, it masks step i+1 and takes its max.
@@ -529,17 +561,28 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) ms[ct] = m_run[ct] * scale;
         half8_t pa[2][2];
-        // scores of step i+1 | P of step i, pair 0
-        if (more) scores(k_read, xn);
-        probs(xc, ms, 0, pa);
-        probs(xc, ms, 1, pa);
-        // P.V of both pairs | mask and max of step i+1.  The P.V MFMAs run at
-        // raised wave priority, so the SIMD's other wave fills the gaps with
-        // its VALU work.
-        __builtin_amdgcn_s_setprio(1);
-        pv_mfma(v_read, 0, pa);
-        pv_mfma(v_read, 1, pa);
-        __builtin_amdgcn_s_setprio(0);
+        if constexpr (F32IO) {
+            // The f32 entry point: weights as hi + lo fp16 pairs, one tile
+            // pair at a time (pv_mfma_hi_lo), before the scores of step i+1
+            // (with both steps' scores live the registers run out).
+            __builtin_amdgcn_s_setprio(1);
+            pv_mfma_hi_lo(v_read, 0, xc, ms);
+            pv_mfma_hi_lo(v_read, 1, xc, ms);
+            __builtin_amdgcn_s_setprio(0);
+            if (more) scores(k_read, xn);
+        } else {
+            // scores of step i+1 | P of step i, pair 0
+            if (more) scores(k_read, xn);
+            probs(xc, ms, 0, pa);
+            probs(xc, ms, 1, pa);
+            // P.V of both pairs | mask and max of step i+1.  The P.V MFMAs run at
+            // raised wave priority, so the SIMD's other wave fills the gaps with
+            // its VALU work.
+            __builtin_amdgcn_s_setprio(1);
+            pv_mfma(v_read, 0, pa);
+            pv_mfma(v_read, 1, pa);
+            __builtin_amdgcn_s_setprio(0);
+        }
         if (more) {
             if (mask_next) apply_mask(s_begin + i + 1, xn);
             // Lazy rescale: m_run is the exponent reference of the column,
@@ -680,7 +723,9 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attention_kernel(Prefi
     // one 2- or 4-byte element per lane and store.
     using OutT = std::conditional_t<F32IO, float, uint16_t>;
     constexpr int kChunk = 16 / static_cast<int>(sizeof(OutT));  // outputs per 16-byte chunk
-    OutT *stage = reinterpret_cast<OutT *>(wave == 0 ? sk0 : wave == 1 ? sk1 : wave == 2 ? sv0 : sv1);
+    static_assert(2 * kQueryBlock * kHeadDim * sizeof(OutT) <= sizeof(sk0),
+                  "a wave's two staged 16 x 128 output tiles fit its own K/V buffer");
+    OutT *stage =reinterpret_cast<OutT *>(wave == 0 ? sk0 : wave == 1 ? sk1 : wave == 2 ? sv0 : sv1);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
 #pragma unroll

@@ -385,9 +385,10 @@ int32_t plan_projection(uint32_t patch_count, uint32_t input_width, uint32_t out
 DecodeShape decode_shape(uint32_t partition_tokens, bool streaming) {
     const uint32_t tiles = (partition_tokens + kBlockTokens - 1) / kBlockTokens;
     if (streaming) return tiles >= 8 ? DecodeShape{4, 1} : DecodeShape{2, 1};
-    // Single shot: the smallest workgroup of 2, 4, 6, 8 or 12 waves holding
-    // one pair of tiles each that covers the partition; longer partitions
-    // loop over 8 waves.
+    // Single shot: the smallest workgroup of 1, 2, 4, 6, 8, 10 or 12 waves
+    // holding one pair of tiles each that covers the partition; longer
+    // partitions loop over 8 waves.
+    if (tiles <= 2) return {1, 1};
     if (tiles <= 4) return {2, 1};
     if (tiles <= 8) return {4, 1};
     if (tiles <= 12) return {6, 1};

@@ -36,6 +36,15 @@ constexpr uint32_t kMaxMergeParts = 64;  // split-K partitions one in-kernel mer
 constexpr uint32_t kTargetWorkgroups = 256;
 constexpr uint32_t kSingleShotTiles = 24;
 constexpr uint32_t kMaxBalancedParts = 16;
+// Arrival counters of the single-shot split-K hand-off count in generations:
+// every partition adds 1 except the one with the highest index, which adds
+// kArrivalSpan - (parts - 1), so a launch adds exactly kArrivalSpan to the
+// counter of each (sequence, kv head) it merges.  The counter is never reset:
+// the arrival that brings it to a multiple of kArrivalSpan is the last, and
+// any value is ready for the next launch (a power of two above the 64
+// partitions a merge combines, so the arithmetic holds modulo 2^32).
+constexpr uint32_t kArrivalSpan = 1024;
+static_assert((kArrivalSpan & (kArrivalSpan - 1)) == 0 && kArrivalSpan > 64, "arrival span");
 // Sequences the ragged (persistent) decode kernel numbers in LDS; launches
 // with more ragged sequences use one workgroup per (partition, head, sequence).
 constexpr uint32_t kMaxRaggedSeqs = 2048;
@@ -309,7 +318,7 @@ struct DecodeWorkspace {
 };
 DecodeWorkspace decode_workspace_layout(uint32_t num_seqs, uint32_t max_parts);
 // Split-K state of one decode launch: partial outputs and (max, sum), merge
-// counters (zero before the launch; every launch leaves them zero), the error
+// counters (zero before the first launch; see kArrivalSpan), the error
 // word and the two status words (automatic streaming partition, compute
 // units).
 struct DecodeState {

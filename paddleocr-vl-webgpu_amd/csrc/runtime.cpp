@@ -53,10 +53,13 @@ struct pvlc_hip_kv_session {
     uint16_t *key_cache = nullptr;    // blocked planes
     uint16_t *value_cache = nullptr;
     float *step_operands = nullptr;  // device: query | key | value (f32, rounded to fp16 by the kernel)
-    float *attention = nullptr;      // device: 16*128 f32
+    // device: 16*128 f32, then the decode workspace in the same allocation,
+    // so one readback of attention + 4 bytes returns the workspace's error
+    // word with the attention
+    float *attention = nullptr;
     void *workspace = nullptr;
+    float *host_staging = nullptr;  // pinned: operands in, attention and error word out
     size_t workspace_bytes = 0;
-    float *host_staging = nullptr;  // pinned: operands in, attention out
     // Host: the rows exactly as given, compact [capacity][2][128] f32 (the
     // descriptor's planes, then each committed step's appended row).  The
     // device planes hold these rounded to fp16; finish returns these.
@@ -133,8 +136,7 @@ void free_session_buffers(pvlc_hip_kv_session *s) {
     (void)hipFree(s->key_cache);
     (void)hipFree(s->value_cache);
     (void)hipFree(s->step_operands);
-    (void)hipFree(s->attention);
-    (void)hipFree(s->workspace);
+    (void)hipFree(s->attention);  // also holds the workspace
     (void)hipHostFree(s->host_staging);
     s->key_cache = s->value_cache = nullptr;
     s->step_operands = s->attention = nullptr;
@@ -228,6 +230,19 @@ pvlc_hip_status validate_decode_geometry(const pvlc_hip_paged_decode_args *a, ui
     if (max_parts > kMaxMergeParts)
         return invalid(PVLC_HIP_INV_INVALID_DECODER_GEOMETRY,
                        "the context needs more than the 64 partitions one merge combines");
+    {
+        // The kernels read the query and the cache planes as 16-byte vectors
+        // and the split-K state with 16-byte buffer accesses; every operand
+        // is held to the same rule, in both operand widths.
+        const void *rows[] = {a->query,  a->new_key, a->new_value, a->out, a->key_cache, a->value_cache,
+                              a->workspace, f32 ? f32->query : nullptr, f32 ? f32->new_key : nullptr,
+                              f32 ? f32->new_value : nullptr, f32 ? f32->out : nullptr};
+        for (const void *r : rows)
+            if (reinterpret_cast<uintptr_t>(r) % 16 != 0)
+                return invalid(PVLC_HIP_INV_LENGTH_MISMATCH,
+                               "paged decode query, new key, new value, output, cache planes and workspace must be "
+                               "16-byte aligned");
+    }
     if (partition_out) *partition_out = partition;
     if (max_parts_out) *max_parts_out = max_parts;
     return PVLC_HIP_OK;
@@ -316,9 +331,10 @@ pvlc_hip_status create_session(pvlc_hip_runtime *rt, const pvlc_hip_kv_session_p
     if ((e = hipMalloc(&s->key_cache, plane_elems * 2)) != hipSuccess) return cleanup(hip_fail(e, "key cache"));
     if ((e = hipMalloc(&s->value_cache, plane_elems * 2)) != hipSuccess) return cleanup(hip_fail(e, "value cache"));
     if ((e = hipMalloc(&s->step_operands, kStepElems * 4)) != hipSuccess) return cleanup(hip_fail(e, "operands"));
-    if ((e = hipMalloc(&s->attention, kQueryElems * 4)) != hipSuccess) return cleanup(hip_fail(e, "attention"));
-    if ((e = hipMalloc(&s->workspace, s->workspace_bytes)) != hipSuccess) return cleanup(hip_fail(e, "workspace"));
-    if ((e = hipHostMalloc(reinterpret_cast<void **>(&s->host_staging), (kStepElems + kQueryElems) * 4,
+    if ((e = hipMalloc(&s->attention, kQueryElems * 4 + s->workspace_bytes)) != hipSuccess)
+        return cleanup(hip_fail(e, "attention and workspace"));
+    s->workspace = s->attention + kQueryElems;  // 8 KiB in: 256-byte aligned
+    if ((e = hipHostMalloc(reinterpret_cast<void **>(&s->host_staging), (kStepElems + kQueryElems + 1) * 4,
                            hipHostMallocDefault)) != hipSuccess)
         return cleanup(hip_fail(e, "pinned staging"));
 
@@ -396,7 +412,8 @@ pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_oper
     rt->counters.kernel_launches += launches;
 
     float *result = stage + kStepElems;
-    HIP_TRY(hipMemcpyAsync(result, s->attention, kQueryElems * 4, hipMemcpyDeviceToHost, rt->stream),
+    // The attention and, right after it, the workspace's device error word.
+    HIP_TRY(hipMemcpyAsync(result, s->attention, (kQueryElems + 1) * 4, hipMemcpyDeviceToHost, rt->stream),
             "attention readback");
     rt->counters.device_to_host_copies += 1;
     const bool expire = s->expire_next_wait;
@@ -406,6 +423,12 @@ pvlc_hip_status execute_step(pvlc_hip_kv_session *s, const pvlc_hip_kv_step_oper
         s->fail_next_after_submit = false;
         return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE, "decoder KV session step: injected failure after submission");
     }
+    uint32_t device_error = 0;
+    std::memcpy(&device_error, result + kQueryElems, 4);
+    if (device_error != 0)
+        return fail(PVLC_HIP_OPERATION, PVLC_HIP_INV_NONE,
+                    "decoder KV session step: the decode kernel reported device error bits " +
+                        std::to_string(device_error));
     std::memcpy(attention, result, kQueryElems * 4);
     const size_t row = static_cast<size_t>(s->cache_tokens) * kRowElems;
     std::memcpy(s->key_rows.data() + row, step->appended_key, kRowElems * 4);
@@ -449,7 +472,11 @@ pvlc_hip_status read_planes(pvlc_hip_kv_session *s, float *key_out, float *value
     const bool expire = s->expire_next_wait;
     s->expire_next_wait = false;
     if (pvlc_hip_status st = wait_or_fail(rt, expire, "decoder KV session finish")) {
-        release.keep = wait_bounded(rt, false) != hipSuccess;
+        // After a real time-out (or a failed queue) the copies may still write
+        // into the staging: it is kept (leaked) without waiting a second bound.
+        // After the tests' injected expiry one query of the event decides.
+        // The session's release makes the one remaining bounded wait.
+        release.keep = !expire || hipEventQuery(rt->done) != hipSuccess;
         return st;
     }
     auto same = [](uint16_t device, float row) { return device == f32_to_f16_rne(row); };

@@ -8,6 +8,7 @@ import sys
 import numpy as np
 
 import oracle as O
+from oracle.comparison import NATIVE_DECODE_POLICY, compare_f32  # noqa: F401 (re-exported)
 from __graft_entry__ import load_package
 
 pvlc = load_package()
@@ -25,17 +26,23 @@ def widen(bits):
     return O.f16_to_f32(bits)
 
 
-def check_close(actual, expected, label="", atol=ATOL, rel=REL_L2):
+def check_close(actual, expected, label="", atol=ATOL, rel=REL_L2, policy=None):
+    """The reference's comparison report (compare_f32, crates/pvlc-testkit/src/lib.rs:69-170, restated in
+    oracle/comparison.py): every metric is printed; the north-star bound (max-abs `atol`, relative L2 `rel`) is
+    asserted, and with `policy` (a ComparisonPolicy, e.g. the reference's native decode policy) every metric of
+    that policy as well.  Returns (max_abs, rel_l2)."""
     actual = np.asarray(actual, np.float32).ravel()
     expected = np.asarray(expected, np.float32).ravel()
     assert np.all(np.isfinite(actual)), f"{label}: non-finite output"
-    err = np.abs(actual - expected)
-    max_abs = float(err.max())
-    rel_l2 = float(np.linalg.norm(actual - expected) / max(np.linalg.norm(expected), 1e-30))
-    print(f"[parity] {label}: max_abs={max_abs:.3e} rel_l2={rel_l2:.3e}", flush=True)
-    assert max_abs <= atol, f"{label}: max abs {max_abs} > {atol}"
-    assert rel_l2 <= rel, f"{label}: rel L2 {rel_l2} > {rel}"
-    return max_abs, rel_l2
+    r = compare_f32(expected, actual)
+    print(f"[parity] {label}: max_abs={r.max_abs:.3e} mean_abs={r.mean_abs:.3e} p99_abs={r.p99_abs:.3e} "
+          f"rel_l2={r.relative_l2:.3e} cos={r.cosine_similarity:.8f}", flush=True)
+    assert r.max_abs <= atol, f"{label}: max abs {r.max_abs} > {atol}"
+    assert r.relative_l2 <= rel, f"{label}: rel L2 {r.relative_l2} > {rel}"
+    if policy is not None:
+        violations = r.assess(policy)
+        assert not violations, f"{label}: violates {violations} of {policy}"
+    return r.max_abs, r.relative_l2
 
 
 def key_slot(t):

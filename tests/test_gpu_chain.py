@@ -3,7 +3,7 @@ single-layer paged decode (rotary on q and the new key, append, GQA), the o GEMV
 down GEMV, then the LM head fused with the greedy top-1 -- the per-layer chain the reference's stack session
 issues (crates/pvlc-runtime-web/src/web/decoder_stack_session.rs:4625-4797).  The decode runs on the f32 operands
 the projections write (pvlc_hip_paged_decode_f32io), or through fp16 conversions and the fp16 entry point.
-Checks, at 3 layers and T=300:
+Checks, at 3 layers and T=300 and at the bench's shape (18 layers, T=2048, the 103424-row LM head):
 
 - every layer's attention against decode_gqa_f32 (cpu-ref lib.rs:858-927) over that layer's cached rows plus
   the appended row, on the q|k|v the chain computed (q rotated with apply_rope_neox and rounded to fp16 -- from
@@ -24,12 +24,14 @@ from pvlc_testlib import W, check_close, from_dev, log, pvlc, rope_k_f16, widen
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("f32_operands", [True, False])
-def test_token_chain_against_the_oracle_and_replayed_from_a_graph(f32_operands):
+@pytest.mark.parametrize("layers,context,capacity,head_rows,f32_operands",
+                         [(3, 300, 320, 20_000, True), (3, 300, 320, 20_000, False),
+                          (18, 2048, 2304, 103_424, True), (18, 2048, 2304, 103_424, False)])
+def test_token_chain_against_the_oracle_and_replayed_from_a_graph(layers, context, capacity, head_rows,
+                                                                  f32_operands):
     import torch
-    layers, context, capacity = 3, 300, 320
     log(f"case: decoder token chain, {layers} layers, T={context}, f32 operands {f32_operands}")
-    chain = bench.TokenChain(pvlc, torch, layers, context, capacity, head_rows=20_000, seed=5,
+    chain = bench.TokenChain(pvlc, torch, layers, context, capacity, head_rows=head_rows, seed=5,
                              f32_operands=f32_operands)
     stream = torch.cuda.current_stream()
     before = []

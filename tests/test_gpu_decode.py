@@ -12,8 +12,8 @@ import numpy as np
 import pytest
 
 import oracle as O
-from pvlc_testlib import (W, check_close, f16_bits, from_dev, gather_rows, log, pvlc, rope_k_f16, scatter_rows,
-                          to_dev, to_dev_f32, to_dev_i32, widen)
+from pvlc_testlib import (NATIVE_DECODE_POLICY, W, check_close, f16_bits, from_dev, gather_rows, log, pvlc, rope_k_f16,
+                          scatter_rows, to_dev, to_dev_f32, to_dev_i32, widen)
 
 pytestmark = pytest.mark.gpu
 POISON = np.array([0x7FC051A7], np.uint32).view(np.float32)[0]  # runtime-core lib.rs:184
@@ -52,7 +52,8 @@ def test_session_single_step_config1_shape(runtime):
     assert ex.cache_tokens == prefix + 1 and s.cache_tokens == prefix + 1
     ka = np.concatenate([keys[:prefix * W], k])
     va = np.concatenate([values[:prefix * W], v])
-    check_close(ex.attention, O.decode_gqa_f32(q, ka, va, prefix + 1, 16, 2, 128), "session T=1025")
+    check_close(ex.attention, O.decode_gqa_f32(q, ka, va, prefix + 1, 16, 2, 128), "session T=1025",
+                policy=NATIVE_DECODE_POLICY)
     snap = s.finish()
     assert snap.cache_tokens == prefix + 1 and snap.cache_capacity == capacity
     np.testing.assert_array_equal(bits32(snap.key_cache[:(prefix + 1) * W]), bits32(ka))
@@ -87,7 +88,8 @@ def test_session_finish_returns_f32_rows_as_given(runtime, prefix, capacity):
         out = s.step(pvlc.DecoderKvSessionStep(q, k, v)).attention
         ka, va = np.concatenate([ka, k]), np.concatenate([va, v])
         t = prefix + 1 + i
-        check_close(out, O.decode_gqa_f32(rounded(q), rounded(ka), rounded(va), t, 16, 2, 128), f"step {i} T={t}")
+        check_close(out, O.decode_gqa_f32(rounded(q), rounded(ka), rounded(va), t, 16, 2, 128), f"step {i} T={t}",
+                    policy=NATIVE_DECODE_POLICY)
     snap = s.finish()
     assert snap.cache_tokens == prefix + 3
     np.testing.assert_array_equal(bits32(snap.key_cache[:(prefix + 3) * W]), bits32(ka))
@@ -105,7 +107,8 @@ def test_session_prefix_sweep(runtime, prefix):
     out = s.step(pvlc.DecoderKvSessionStep(q, k, v)).attention
     ka = np.concatenate([keys[:prefix * W], k])
     va = np.concatenate([values[:prefix * W], v])
-    check_close(out, O.decode_gqa_f32(q, ka, va, prefix + 1, 16, 2, 128), f"prefix={prefix}")
+    check_close(out, O.decode_gqa_f32(q, ka, va, prefix + 1, 16, 2, 128), f"prefix={prefix}",
+                policy=NATIVE_DECODE_POLICY)
 
 
 def test_session_persistent_steps_and_finish_snapshot(runtime):
@@ -119,7 +122,7 @@ def test_session_persistent_steps_and_finish_snapshot(runtime):
         out = s.step(pvlc.DecoderKvSessionStep(q, k, v)).attention
         ka, va = np.concatenate([ka, k]), np.concatenate([va, v])
         t = prefix + 1 + i
-        check_close(out, O.decode_gqa_f32(q, ka, va, t, 16, 2, 128), f"step {i} T={t}")
+        check_close(out, O.decode_gqa_f32(q, ka, va, t, 16, 2, 128), f"step {i} T={t}", policy=NATIVE_DECODE_POLICY)
     snap = s.finish()
     assert snap.cache_tokens == prefix + steps
     np.testing.assert_array_equal(bits32(snap.key_cache[:(prefix + steps) * W]), bits32(ka))
@@ -297,7 +300,8 @@ def test_cached_gqa_one_shot(runtime):
     assert ex.cache_tokens == prefix + 1 and ex.cache_capacity == capacity
     ka = np.concatenate([keys[:prefix * W], k])
     va = np.concatenate([values[:prefix * W], v])
-    check_close(ex.attention, O.decode_gqa_f32(q, ka, va, prefix + 1, 16, 2, 128), "cached gqa")
+    check_close(ex.attention, O.decode_gqa_f32(q, ka, va, prefix + 1, 16, 2, 128), "cached gqa",
+                policy=NATIVE_DECODE_POLICY)
     np.testing.assert_array_equal(bits32(ex.key_cache[:(prefix + 1) * W]), bits32(ka))
     np.testing.assert_array_equal(bits32(ex.value_cache[:(prefix + 1) * W]), bits32(va))
 
@@ -401,6 +405,37 @@ def test_config2_sweep_automatic_shapes(prefix, planned):
     log(f"case: config 2 sweep shape T={prefix + 1} (automatic partition {planned})")
     r = device_decode(18, prefix, 2304, seed=3000 + prefix)
     check_device_layers(r, 18, prefix, label=f"sweep T={prefix + 1}")
+
+
+@pytest.mark.parametrize("layers,prefix,partition", [(1, 2047, 0), (1, 2047, 32), (1, 1999, 32), (1, 2047, 64),
+                                                     (1, 299, 16), (1, 1024, 128), (1, 4095, 64), (4, 2047, 0),
+                                                     (2, 700, 48), (1, 127, 16)])
+def test_many_partitions_and_one_wave_partitions(layers, prefix, partition):
+    """Single-shot launches with up to 64 partitions per (layer, kv head) -- the last to arrive merges them all
+    (16-byte partials, batches of 4 partials with the 16 elements a thread of the one-wave shape owns) -- and
+    partitions of one or two tiles, which run on one-wave workgroups.  Every layer against the oracle, caches
+    bit-exact."""
+    log(f"case: many partitions layers={layers} T={prefix + 1} partition={partition}")
+    r = device_decode(layers, prefix, prefix + 1, seed=4100 + prefix + partition, partition=partition)
+    check_device_layers(r, layers, prefix, label=f"parts T={prefix + 1} p={partition}")
+
+
+def test_arrival_counters_across_launches():
+    """One workspace through launches whose partition counts change from launch to launch (up to 64 partitions,
+    single partitions between them): the arrival counters are never reset -- every launch adds one generation
+    (1024) to each counter it uses -- so every launch finds them ready whatever the previous one left."""
+    import torch
+    capacity = 2048
+    wsb = pvlc.decode_workspace_bytes(2, capacity, 32)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    pvlc.workspace_init(ws, wsb)
+    for i, (prefix, partition) in enumerate([(2047, 32), (2047, 512), (100, 0), (1500, 48), (33, 32), (2040, 0),
+                                             (15, 0), (2047, 64), (999, 320), (2047, 0)]):
+        log(f"case: shared workspace launch {i}: T={prefix + 1} partition={partition}")
+        r = device_decode(2, prefix, capacity, seed=4300 + i, partition=partition, workspace=(ws, wsb))
+        check_device_layers(r, 2, prefix, label=f"shared ws {i} T={prefix + 1} p={partition}")
+    counters = ws[256:256 + 16].view(torch.int32).cpu().numpy()
+    assert np.all(counters % 1024 == 0) and np.all(counters > 0), counters
 
 
 def test_rotated_query_and_explicit_positions():

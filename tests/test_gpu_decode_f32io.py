@@ -3,20 +3,23 @@ the format the reference's chain passes between its dispatches (decoder_mrope_f3
 q/k/v, decoder_gqa_split_merge_f32 writes the f32 output the o projection reads; pvlc-wgsl lib.rs:1024-1234,
 web decoder_stack_session.rs:4698-4729).
 
-- With inputs that fp16 holds exactly, the f32 entry point is the fp16 one: the caches it leaves are bit-identical
-  and its f32 output rounds (RNE) to the fp16 entry point's output bit for bit -- in the single-shot regime
-  (18 layers, T=2048, the in-kernel merge), with one partition (no merge), and in the streaming regime (ragged
-  paged batch: persistent kernel + merge kernel).
+- With inputs that fp16 holds exactly, the caches the f32 entry point leaves are bit-identical to the fp16 entry
+  point's -- in the single-shot regime (18 layers, T=2048, the in-kernel merge), with one partition (no merge),
+  and in the streaming regime (ragged paged batch: persistent kernel + merge kernel).  Its f32 output carries
+  the softmax weights as hi + lo fp16 pairs, so on every sequence it meets the reference's native decode policy
+  against decode_gqa_f32 (max-abs 4e-4, mean 6e-5, p99 2.5e-4, relative L2 1.5e-4, cosine 0.99999;
+  decoder_cached_gqa_native_contract.rs:147-158); the fp16 entry point (fp16 weights, fp16 output) stays within
+  the north-star bound of it.
 - With general f32 inputs the query and the new key are rotated from their f32 values and rounded once: the
   appended key row equals the oracle's apply_rope_neox of the f32 key rounded to fp16, bit for bit, and the
-  output is within the decode tolerance of decode_gqa_f32 over the query rotated and rounded the same way."""
+  output meets the native policy against decode_gqa_f32 over the query rotated and rounded the same way."""
 
 import numpy as np
 import pytest
 
 import oracle as O
-from pvlc_testlib import W, check_close, f16_bits, from_dev, gather_rows, log, pvlc, scatter_rows, to_dev, \
-    to_dev_f32, to_dev_i32, widen
+from pvlc_testlib import NATIVE_DECODE_POLICY, W, check_close, f16_bits, from_dev, gather_rows, log, pvlc, \
+    scatter_rows, to_dev, to_dev_f32, to_dev_i32, widen
 
 pytestmark = pytest.mark.gpu
 
@@ -96,8 +99,8 @@ def launch(case, q, nk, nv, f32, rotate_query, partition=0, uniform=False):
     ("12 ragged paged sequences (streaming + merge kernel)", [1, 17, 300, 900, 1500, 2047, 2048, 2500, 3000, 64,
                                                                129, 777], True, False, True),
 ])
-def test_f32_operands_match_the_fp16_entry_point_bit_for_bit(label, lens, paged, uniform, rotate_query):
-    log(f"case: f32 operands vs fp16 entry point, {label}")
+def test_f32_operands_leave_the_fp16_caches_and_meet_the_native_policy(label, lens, paged, uniform, rotate_query):
+    log(f"case: f32 operands vs fp16 entry point and the oracle, {label}")
     case = build_case(lens, seed=len(lens) * 7 + 3, paged=paged)
     n = case["num_seqs"]
     q, nk, nv = f16_bits(11, n * 2048), f16_bits(12, n * W), f16_bits(13, n * W)
@@ -106,7 +109,16 @@ def test_f32_operands_match_the_fp16_entry_point_bit_for_bit(label, lens, paged,
     np.testing.assert_array_equal(k32, k16)
     np.testing.assert_array_equal(v32, v16)
     assert np.all(np.isfinite(out32))
-    np.testing.assert_array_equal(O.f32_to_f16(out32), out16)
+    for s in range(n):
+        t = int(case["cache_lens"][s])
+        gk, gv = gather_rows(k32, v32, t + 1, case["tables"][s])
+        qs = widen(q[s * 2048:(s + 1) * 2048])
+        if rotate_query:
+            qs = widen(O.f32_to_f16(O.rope_neox_f32(qs, 16, 128, 128, [t] * 16, 500000.0)))
+        want = O.decode_gqa_f32(qs, widen(gk), widen(gv), t + 1, 16, 2, 128)
+        check_close(out32[s * 2048:(s + 1) * 2048], want, f"{label}: f32 output seq {s}", policy=NATIVE_DECODE_POLICY)
+        check_close(widen(out16[s * 2048:(s + 1) * 2048]), out32[s * 2048:(s + 1) * 2048],
+                    f"{label}: fp16 output seq {s} vs f32 output")
 
 
 def test_f32_operands_are_rotated_before_their_rounding():
@@ -127,4 +139,5 @@ def test_f32_operands_are_rotated_before_their_rounding():
         np.testing.assert_array_equal(gv, np.concatenate([case["rows"][s][1], O.f32_to_f16(nv[s * W:(s + 1) * W])]))
         q_rot = O.f32_to_f16(O.rope_neox_f32(q[s * 2048:(s + 1) * 2048], 16, 128, 128, [t] * 16, 500000.0))
         want = O.decode_gqa_f32(widen(q_rot), widen(gk), widen(gv), t + 1, 16, 2, 128)
-        check_close(out[s * 2048:(s + 1) * 2048], want, f"f32 operands seq {s} T={t + 1}")
+        check_close(out[s * 2048:(s + 1) * 2048], want, f"f32 operands seq {s} T={t + 1}",
+                    policy=NATIVE_DECODE_POLICY)

@@ -136,6 +136,44 @@ def test_split_and_unsplit_schedules_agree_and_the_workspace_is_reusable():
     assert int(counters.abs().sum().item()) == 0
 
 
+def causal_gqa_fp32_on_device(qr, kr, vr, n):
+    """An fp32 restatement of causal_gqa_f32 (cpu-ref lib.rs:782-853) on the device, one query head at a time:
+    scores Q_h K_g^T / sqrt(128) in f32 (query head h reads kv head h // 8), future keys masked, f32 softmax,
+    then P V_g.  Inputs are the oracle's rotated f32 query and the fp16 keys and values widened; the products
+    run on torch's f32 GEMM (no reduced-precision mode)."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    q = torch.from_numpy(qr.reshape(n, 16, 128)).cuda()
+    k = torch.from_numpy(kr.reshape(n, 2, 128)).cuda()
+    v = torch.from_numpy(vr.reshape(n, 2, 128)).cuda()
+    future = torch.triu(torch.ones(n, n, dtype=torch.bool, device="cuda"), diagonal=1)
+    out = torch.empty(n, 16, 128, device="cuda")
+    for h in range(16):
+        g = h // 8
+        s = torch.matmul(q[:, h, :].contiguous(), k[:, g, :].t().contiguous()) / np.sqrt(128.0)
+        s.masked_fill_(future, float("-inf"))
+        out[:, h, :] = torch.matmul(torch.softmax(s, dim=1), v[:, g, :].contiguous())
+    return out.reshape(-1).cpu().numpy()
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_config4_every_row_and_a_row_of_every_query_block(split):
+    """Config 4 (N=4096) in full, in both schedules: every row of the output against the fp32 restatement on
+    the device, and one row of each of the 256 query blocks (position 16b + b mod 16) against the oracle through
+    the identity `row i of causal == decode over i + 1 keys` (decoder_decode_contract.rs:888-1047) -- so a fault
+    confined to some query blocks or to one side of a split cannot pass."""
+    n = 4096
+    log(f"case: config 4 every row (N=4096, split={split})")
+    ws = prefill_workspace(n) if split else None
+    out, qr, kr, vr, scratch, q = run_prefill(n, seed=4097, workspace=ws)
+    want = causal_gqa_fp32_on_device(qr, kr, vr, n)
+    check_close(out, want, f"config4 split={split} all rows vs fp32 restatement")
+    per_row = np.abs(out - want).reshape(n, 2048).max(axis=1)
+    assert per_row.max() <= 2e-3, f"worst row {int(per_row.argmax())}: {per_row.max()}"
+    rows = [16 * b + b % 16 for b in range(n // 16)]
+    sampled_rows_match_decode(out, qr, kr, vr, n, rows, f"config4 split={split} oracle")
+
+
 @pytest.mark.parametrize("n,split", [(1100, False), (3000, True)])
 def test_scores_rising_along_the_sequence_move_the_softmax_reference(n, split):
     """Keys whose scores grow by ~41 log2 units along the sequence: the running maximum of every query passes

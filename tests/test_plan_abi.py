@@ -215,13 +215,16 @@ def test_decode_workspace_and_partition_rules():
     assert pvlc.decode_workspace_bytes(18, 2048, 48) > 0
 
 
+FAKE = 1 << 20  # a 16-byte-aligned placeholder address, never dereferenced: validation fails first
+
+
 def _workspace_status(num_seqs, max_context, cache_len, workspace_bytes, partition=0):
     """Status of a launch whose only possible validation failure is the workspace size (the launch
     itself fails without a GPU, after validation)."""
     blocks = (max_context + 15) // 16
     args = pvlc.paged_decode_args(num_seqs=num_seqs, num_blocks=num_seqs * blocks, max_blocks_per_seq=blocks,
-                                  key_cache=1, value_cache=1, query=1, new_key=1, new_value=1, out=1,
-                                  workspace=1, workspace_bytes=workspace_bytes, max_context=max_context,
+                                  key_cache=FAKE, value_cache=FAKE, query=FAKE, new_key=FAKE, new_value=FAKE,
+                                  out=FAKE, workspace=FAKE, workspace_bytes=workspace_bytes, max_context=max_context,
                                   uniform_cache_len=cache_len, partition_tokens=partition)
     try:
         pvlc.paged_decode_f16(args)
@@ -249,20 +252,20 @@ def test_auto_workspace_covers_every_uniform_length(num_seqs, max_context):
 
 
 def test_device_entry_points_validate_before_touching_the_gpu():
-    args = pvlc.paged_decode_args(num_seqs=0, num_blocks=1, max_blocks_per_seq=1, key_cache=1, value_cache=1,
-                                  query=1, new_key=1, new_value=1, out=1, workspace=1, workspace_bytes=1 << 20,
+    args = pvlc.paged_decode_args(num_seqs=0, num_blocks=1, max_blocks_per_seq=1, key_cache=FAKE, value_cache=FAKE,
+                                  query=FAKE, new_key=FAKE, new_value=FAKE, out=FAKE, workspace=FAKE, workspace_bytes=1 << 20,
                                   max_context=16)
     with pytest.raises(pvlc.PvlcHipError) as e:
         pvlc.paged_decode_f16(args)
     assert code(e) == ("InvalidInvocation", "ZeroDimension")
-    args = pvlc.paged_decode_args(num_seqs=1, num_blocks=1, max_blocks_per_seq=1, key_cache=1, value_cache=1,
-                                  query=1, new_key=1, new_value=1, out=1, workspace=1, workspace_bytes=1 << 20,
+    args = pvlc.paged_decode_args(num_seqs=1, num_blocks=1, max_blocks_per_seq=1, key_cache=FAKE, value_cache=FAKE,
+                                  query=FAKE, new_key=FAKE, new_value=FAKE, out=FAKE, workspace=FAKE, workspace_bytes=1 << 20,
                                   max_context=32)
     with pytest.raises(pvlc.PvlcHipError) as e:
         pvlc.paged_decode_f16(args)
     assert code(e) == ("InvalidInvocation", "InvalidDecoderGeometry")
-    args = pvlc.paged_decode_args(num_seqs=1, num_blocks=4, max_blocks_per_seq=4, key_cache=1, value_cache=1,
-                                  query=1, new_key=1, new_value=1, out=1, workspace=1, workspace_bytes=16,
+    args = pvlc.paged_decode_args(num_seqs=1, num_blocks=4, max_blocks_per_seq=4, key_cache=FAKE, value_cache=FAKE,
+                                  query=FAKE, new_key=FAKE, new_value=FAKE, out=FAKE, workspace=FAKE, workspace_bytes=16,
                                   max_context=64, uniform_cache_len=10)
     with pytest.raises(pvlc.PvlcHipError) as e:
         pvlc.paged_decode_f16(args)
@@ -324,6 +327,28 @@ def test_f32_operand_decode_rejects_mixed_or_missing_operands():
     with pytest.raises(pvlc.PvlcHipError) as e:
         pvlc.paged_decode_f16(bare)
     assert code(e) == ("InvalidInvocation", "LengthMismatch")
+
+
+@pytest.mark.parametrize("operand", ["query", "new_key", "new_value", "out", "key_cache", "value_cache", "workspace"])
+def test_decode_rejects_unaligned_operands(operand):
+    """The decode reads the query and the cache planes as 16-byte vectors and moves split-K partials with 16-byte
+    accesses: an operand that is not 16-byte aligned (a 4-byte-aligned float sub-view, say) is rejected before any
+    GPU effect, in the fp16 and the f32 forms."""
+    common = dict(num_seqs=1, num_blocks=4, max_blocks_per_seq=4, key_cache=FAKE, value_cache=FAKE, query=FAKE,
+                  new_key=FAKE, new_value=FAKE, out=FAKE, workspace=FAKE, workspace_bytes=1 << 20, max_context=64,
+                  uniform_cache_len=10)
+    common[operand] = FAKE + 4
+    with pytest.raises(pvlc.PvlcHipError) as e:
+        pvlc.paged_decode_f16(pvlc.paged_decode_args(**common))
+    assert code(e) == ("InvalidInvocation", "LengthMismatch") and "16-byte aligned" in str(e.value)
+    if operand in ("query", "new_key", "new_value", "out"):
+        f32 = dict(query=FAKE, new_key=FAKE, new_value=FAKE, out=FAKE)
+        f32[operand] = FAKE + 4
+        args = pvlc.paged_decode_args(**{**common, operand: FAKE, "query": None, "new_key": None,
+                                         "new_value": None, "out": None})
+        with pytest.raises(pvlc.PvlcHipError) as e:
+            pvlc.paged_decode_f32io(args, f32["query"], f32["new_key"], f32["new_value"], f32["out"])
+        assert code(e) == ("InvalidInvocation", "LengthMismatch") and "16-byte aligned" in str(e.value)
 
 
 def test_f32_operand_prefill_rejects_mixed_or_missing_operands():

@@ -131,3 +131,56 @@ def test_no_alloc_rejects_launches_beyond_its_scratch():
     assert e.value.invocation_code == "LengthMismatch" and "takes no workspace" in str(e.value)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
+
+
+def _first_call_captured_child():
+    """Body of the child process of test_no_alloc_first_call_inside_graph_capture: the process's first
+    no-alloc call is made while torch captures its stream into a HIP graph."""
+    import torch
+    from pvlc_testlib import to_dev, to_dev_f32, to_dev_i32
+    case = make_case(4, [2048] * 4, seed=36, paged=False)
+    ref_out, ref_k, ref_v, ref_err = launch(case, no_alloc=False)  # workspace entry point, fresh caches
+    assert ref_err == 0
+    d_k, d_v = to_dev(case["kp"]), to_dev(case["vp"])
+    out = torch.zeros(case["num_seqs"] * 2048, dtype=torch.int16, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cos, sin = pvlc.rope_table(BASE, case["max_context"])
+    keep = [to_dev(case["q"]), to_dev(case["nk"]), to_dev(case["nv"]), to_dev_f32(cos), to_dev_f32(sin)]
+    args = pvlc.paged_decode_args(num_seqs=case["num_seqs"], num_blocks=case["num_blocks"],
+                                  max_blocks_per_seq=case["max_blocks"], key_cache=d_k, value_cache=d_v,
+                                  query=keep[0], new_key=keep[1], new_value=keep[2], out=out, workspace=None,
+                                  workspace_bytes=0, max_context=case["max_context"], rope_cos=keep[3],
+                                  rope_sin=keep[4], rope_rows=case["max_context"],
+                                  uniform_cache_len=int(case["cache_lens"][0]))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        pvlc.paged_decode_f16_no_alloc(args, err, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    for i in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0, f"replay {i}: device error bits {int(err.item())}"
+        np.testing.assert_array_equal(from_dev(out), ref_out, err_msg=f"replay {i}: attention differs")
+        np.testing.assert_array_equal(from_dev(d_k), ref_k, err_msg=f"replay {i}: key plane differs")
+        np.testing.assert_array_equal(from_dev(d_v), ref_v, err_msg=f"replay {i}: value plane differs")
+        torch.randn(1 << 20, device="cuda").sum().item()  # eager work between replays
+    print("capture child ok", flush=True)
+
+
+def test_no_alloc_first_call_inside_graph_capture():
+    """A fresh process whose first no-alloc call (the per-device set-up included) is made under HIP graph
+    capture: the set-up launches and waits for nothing, so the call is captured like any other, and three
+    replays (eager work and synchronisations between them) equal the workspace entry point bit for bit."""
+    import os
+    import subprocess
+    import sys
+    log("case: no-alloc first call inside graph capture (child process)")
+    here = os.path.dirname(os.path.abspath(__file__))
+    code = (f"import sys; sys.path[:0] = [{here!r}, {os.path.dirname(here)!r}]; "
+            "import test_zz_no_alloc as t; t._first_call_captured_child()")
+    proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=100)
+    print(proc.stdout[-2000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0, f"child failed ({proc.returncode}): {proc.stderr[-1500:]}"
+    assert "capture child ok" in proc.stdout
