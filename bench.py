@@ -114,7 +114,8 @@ def main() -> int:
         extra = argparse.Namespace(**vars(args))
         extra.cpu_seconds = args.cpu_seconds_extra
         torch.cuda.empty_cache()
-        result["configs"] = {}
+        result["configs"] = {"config1": measure_config1(pvlc, torch, extra)}
+        torch.cuda.empty_cache()
         for c in (3, 5):
             result["configs"][f"config{c}"] = measure_batched(pvlc, torch, c, extra)
             torch.cuda.empty_cache()
@@ -219,15 +220,7 @@ def measure_config2(pvlc, torch, args):
     gbps = step_bytes / (ms_per_step * 1e-3) / 1e9
     warm_gbps = step_bytes / (warm_ms * 1e-3) / 1e9
 
-    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    # runs (scaled by a copy of known size); see the summary beside it.
-    traffic = None
-    tpath = os.path.join(REPO, "profiles", "decode18_t2048_traffic.txt")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            for line in f:
-                if line.startswith("hbm_bytes_per_launch"):
-                    traffic = int(line.split("=")[1])
+    traffic, traffic_source = profiled_traffic("decode18_t2048_traffic.txt")
 
     result = {
         "metric": "decode-attn µs/step + achieved HBM GB/s (% peak), 18 layers, 2k ctx, 1 GPU",
@@ -255,7 +248,7 @@ def measure_config2(pvlc, torch, args):
                                         "Cache, not HBM"},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "algorithmic_bytes_per_launch": step_bytes},
+                     "traffic_source": traffic_source, "algorithmic_bytes_per_launch": step_bytes},
         "device_error_word": err,
         "timed_wall_s": round(wall, 3),
     }
@@ -289,6 +282,121 @@ def measure_config2(pvlc, torch, args):
     return result
 
 
+def profiled_traffic(name):
+    """HBM bytes per launch of a kernel from its committed rocprofv3 FETCH_SIZE + WRITE_SIZE runs (each scaled by
+    the same counter's reading for a copy of known size), as written to profiles/<name>: (bytes, source), or
+    (None, None) without the file.  The figure is a measured constant of the build the profile names, not a
+    measurement of this run."""
+    path = os.path.join(REPO, "profiles", name)
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch"):
+                return int(line.split("=")[1]), (f"profiles/{name}: rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, "
+                                                 "scaled by a 256 MiB copy; measured in a profile run, not this one")
+    return None, None
+
+
+def measure_config1(pvlc, torch, args, replicas=300, reps=7):
+    """Config 1 (the CPU-path case): one decoder layer, prefix 1024, the new token's K
+    rotated at position 1024 (base 500000) and appended, GQA over T = 1025 rows.  GPU: the fused decode launch
+    (pvlc_hip_paged_decode_f16, one sequence) timed over launches that rotate `replicas` caches (~300 MB, so
+    each reads HBM rather than the Infinity Cache), and the session step (pvlc_hip_kv_session_step: f32
+    operands copied in, the attention copied out, synchronised) -- the reference's round-trip API, PCIe
+    included.  CPU: the oracle's rope_neox + append_decoder_kv_cache + decode_gqa_f32, single thread, median of
+    `reps` repetitions."""
+    import oracle as O
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    prefix, context, capacity = 1024, 1025, 1040
+    nb = (capacity + 15) // 16
+    rng = np.random.default_rng(1)
+    keys = rng.standard_normal(capacity * W).astype(np.float32).astype(np.float16)
+    values = rng.standard_normal(capacity * W).astype(np.float32).astype(np.float16)
+    q = rng.standard_normal(2048).astype(np.float32).astype(np.float16)
+    nk = rng.standard_normal(W).astype(np.float32).astype(np.float16)
+    nv = rng.standard_normal(W).astype(np.float32).astype(np.float16)
+    kp0 = torch.empty(nb * 16 * W, dtype=torch.float16, device=dev)
+    vp0 = torch.empty_like(kp0)
+    pvlc.kv_pack_f16(torch.from_numpy(keys).to(dev), torch.from_numpy(values).to(dev), prefix, kp0, vp0, nb)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    planes = [(kp0, vp0)] + [(torch.randn(nb * 16 * W, generator=gen, device=dev).half(),
+                              torch.randn(nb * 16 * W, generator=gen, device=dev).half()) for _ in range(replicas - 1)]
+    d_q, d_nk, d_nv = (torch.from_numpy(x).to(dev) for x in (q, nk, nv))
+    out = torch.empty(2048, dtype=torch.float16, device=dev)
+    cos, sin = pvlc.rope_table(ROPE_BASE, capacity)
+    d_cos, d_sin = torch.from_numpy(cos.ravel()).to(dev), torch.from_numpy(sin.ravel()).to(dev)
+    wsb = pvlc.decode_workspace_bytes(1, capacity)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    pvlc.workspace_init(ws, wsb, stream)
+    launches = [pvlc.paged_decode_args(num_seqs=1, num_blocks=nb, max_blocks_per_seq=nb, key_cache=kp, value_cache=vp,
+                                       query=d_q, new_key=d_nk, new_value=d_nv, out=out, workspace=ws,
+                                       workspace_bytes=wsb, max_context=capacity, uniform_cache_len=prefix,
+                                       rope_cos=d_cos, rope_sin=d_sin, rope_rows=capacity) for kp, vp in planes]
+    steps = max(args.steps, 200)
+    for i in range(args.warmup):
+        pvlc.paged_decode_f16(launches[i % replicas], stream)
+    ms = _timed_launches(torch, stream, steps, lambda i: pvlc.paged_decode_f16(launches[i % replicas], stream))
+    stats = _launch_stats(torch, stream, steps, lambda i: pvlc.paged_decode_f16(launches[i % replicas], stream))
+    pvlc.paged_decode_f16(launches[0], stream)
+    torch.cuda.synchronize()
+    gpu_out = out.float().cpu().numpy()
+    err = pvlc.workspace_error(ws, wsb, stream)
+    step_bytes = algorithmic_bytes(context)
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+
+    # The session round trip (host f32 operands in, f32 attention out) on the same cache rows.
+    runtime = pvlc.NativeRuntime(0)
+    kf, vf = keys.astype(np.float32), values.astype(np.float32)
+    sess_times = []
+    for _ in range(reps):
+        session = runtime.begin_decoder_kv_session(pvlc.DecoderKvSessionDescriptor(prefix, capacity, kf, vf))
+        step = pvlc.DecoderKvSessionStep(q.astype(np.float32), nk.astype(np.float32), nv.astype(np.float32))
+        t0 = time.perf_counter()
+        session.step(step)
+        sess_times.append(time.perf_counter() - t0)
+        session.finish()
+    runtime.close()
+
+    result = {"metric": "single-layer decode step µs (rotary K append + GQA over T=1025)",
+              "config": {"workload": "config 1: one decoder layer, prefix 1024, append at position 1024 (rotary "
+                                     "base 500000), GQA 16q/2kv d128 over 1025 rows", "context": context,
+                         "cache_replicas_rotated": replicas,
+                         "partition_tokens": pvlc.decode_partition(1, context)},
+              "value": round(ms * 1e3, 3), "unit": "µs/step", "steps": steps, "warmup": args.warmup,
+              "achieved_gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+              "launch_stats": stats, "algorithmic_bytes": step_bytes, "device_error_word": err,
+              "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                           "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+              "session_step_us": {"median": round(float(np.median(sess_times)) * 1e6, 1),
+                                  "reps": reps,
+                                  "note": "pvlc_hip_kv_session_step: 9 KiB of f32 operands in, 8 KiB of attention "
+                                          "out, one synchronisation (PCIe-inclusive round trip; never the bench "
+                                          "value)"},
+              "inputs": {"generator": "numpy PCG64 standard_normal -> f32 -> fp16 (replica 0, the CPU inputs), "
+                                      "torch Philox randn (replicas 1..)", "seeds": {"numpy": 1, "torch": 1}}}
+    if not args.no_cpu:
+        qf, nkf, nvf = q.astype(np.float32), nk.astype(np.float32), nv.astype(np.float32)
+        times, cpu_out = [], None
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            rot = O.rope_neox_f32(nkf, 2, 128, 128, [prefix, prefix], ROPE_BASE)
+            rot = O.f16_to_f32(O.f32_to_f16(rot))  # stored as fp16, like the device cache
+            k_all, v_all = O.append_kv_f32(kf[:prefix * W], vf[:prefix * W], prefix, rot, nvf, 2, 128)
+            cpu_out = O.decode_gqa_f32(qf, k_all, v_all, context, 16, 2, 128)
+            times.append(time.perf_counter() - t0)
+        per_step = float(np.median(times))
+        result["cpu_baseline"] = {"value": round(per_step * 1e6, 1), "unit": "µs/step", "cores": 1, "kind": "port",
+                                  "gbps": round(step_bytes / per_step / 1e9, 3),
+                                  "sample": f"median of {reps} full steps (rope + append + decode_gqa_f32, T=1025)",
+                                  "host": host_cpu_info(),
+                                  "gpu_vs_cpu_max_abs": float(np.max(np.abs(gpu_out - cpu_out)))}
+    del planes, launches
+    return result
+
+
 def calibrate_copy(args):
     """Plain device copy of 256 MiB (reads 256 MiB, writes 256 MiB per launch),
     run under rocprofv3 --pmc to convert FETCH_SIZE / WRITE_SIZE to bytes."""
@@ -318,13 +426,13 @@ def _timed_launches(torch, stream, k, fn):
     return start.elapsed_time(end) / k
 
 
-def _launch_stats(torch, stream, k, fn, group=10):
-    """Spread of the per-launch time over k back-to-back calls of fn(i) on `stream`: the calls run as k // group
-    groups of `group` launches, each group between one event pair (queued behind a GPU-side delay), and each
-    group gives one per-launch time (median, p10, p90 over the groups).  An event between every two launches
-    would add its own marker (~2.7 µs measured on a 12.7 µs decode step), so single launches are not timed
-    apart."""
-    groups = max(1, k // group)
+def _launch_stats(torch, stream, k, fn, group=10, min_groups=20):
+    """Spread of the per-launch time over back-to-back calls of fn(i) on `stream`: max(k, group * min_groups)
+    calls (at least 200 whatever --steps is, so the percentiles rest on at least 20 samples) run as groups of
+    `group` launches, each group between one event pair (queued behind a GPU-side delay), and each group gives
+    one per-launch time (median, p10, p90 over the groups).  An event between every two launches would add its
+    own marker (~2.7 µs measured on a 12.7 µs decode step), so single launches are not timed apart."""
+    groups = max(min_groups, k // group)
     torch.cuda.synchronize()
     torch.cuda._sleep(int(2_000_000 + 60_000 * groups * group))
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
@@ -434,6 +542,9 @@ def measure_batched(pvlc, torch, config, args):
         "algorithmic_bytes": step_bytes, "device_error_word": pvlc.workspace_error(ws, wsb, stream),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None}}
+    traffic, source = profiled_traffic(f"batched_decode_config{config}_traffic.txt")
+    if traffic is not None:
+        result["roofline"].update(traffic=traffic, traffic_source=source)
     if not part:
         # An automatic streaming launch records the partition it settled on after the error word.
         words = ws[:16].cpu().numpy().view(np.uint32)
