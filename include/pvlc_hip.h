@@ -419,7 +419,10 @@ pvlc_hip_status pvlc_hip_paged_decode_f16(const pvlc_hip_paged_decode_args *args
  * new_value [num_seqs][2][128], out [num_seqs][16][128], all f32 device
  * pointers.  The query and the new key are rotated from their f32 values and
  * rounded to fp16 once (RNE); the new value is rounded to fp16; the cache
- * stays fp16; the output is the f32 quotient the fp16 entry point rounds.
+ * stays fp16.  The softmax weights enter P.V as exact pairs of fp16 values
+ * (hi = fp16(p), lo = fp16(p - hi): ~22 bits), so the f32 output meets the
+ * reference's native comparison policy (decoder_cached_gqa_native_contract.rs:
+ * 147-158) where the fp16 entry point's fp16 weights and output do not.
  * args->query, new_key, new_value and out must be NULL; everything else as
  * pvlc_hip_paged_decode_f16. */
 pvlc_hip_status pvlc_hip_paged_decode_f32io(const pvlc_hip_paged_decode_args *args, const float *query,
@@ -487,9 +490,9 @@ pvlc_hip_status pvlc_hip_paged_prefill_f16(const pvlc_hip_paged_prefill_args *ar
  * [tokens][16][128], all f32 device pointers.  The query and the keys are
  * rotated from their f32 values and rounded to fp16 once (RNE), the values
  * rounded to fp16; the cache (and the optional query scratch) stays fp16; the
- * output is the normalised f32 product o * (1/l), which the fp16 entry point
- * rounds to fp16 once from the exact product.  args->query, key, value and out
- * must be NULL; everything else as pvlc_hip_paged_prefill_f16. */
+ * softmax weights enter P.V as exact hi + lo pairs of fp16 values (~22 bits),
+ * and the output is the normalised f32 product o * (1/l).  args->query, key,
+ * value and out must be NULL; everything else as pvlc_hip_paged_prefill_f16. */
 pvlc_hip_status pvlc_hip_paged_prefill_f32io(const pvlc_hip_paged_prefill_args *args, const float *query,
                                              const float *key, const float *value, float *out, void *stream);
 
