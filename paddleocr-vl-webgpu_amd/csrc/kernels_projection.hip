@@ -22,9 +22,9 @@
 // ring with one barrier per step.  Every load instruction reads long runs:
 // 1 KiB of the activation block, or 16 weight rows x 64 bytes.  Projections
 // with at least 512 tiles of 128 x 256 (gate|up at N=4096) run the wide
-// variant instead (kernel 2b below): 4 waves of 64 x 128, and the tiles of
-// each XCD in one block of the output, so both operands are reused from the
-// XCD's L2.
+// variant instead (kernel 2b below): 128 x 256 or 128 x 192 tiles, 4 waves,
+// and the tiles of each XCD in one block of the output, so both operands are
+// reused from the XCD's L2.
 
 #include <hip/hip_runtime.h>
 
@@ -375,17 +375,17 @@ __global__ __launch_bounds__(kGemmThreads, MIN_WGS) void projection_gemm_kernel(
 }
 
 // Kernel 2b (wide projections: enough 128 x 256 output tiles to give every
-// compute unit two): projection_gemm_wide_kernel, 128 x 256 output tiles, 4
-// waves of 64 x 128 (4 x 8 MFMA tiles, hi and lo), K in steps of 32.  The activation
-// stages (16 KiB) move through a three-stage ring, loaded two steps ahead,
-// the weight stages (16 KiB) through a two-stage ring, loaded one step ahead:
-// 80 KiB, two workgroups per compute unit (160 KiB of LDS).  Per
-// 32-wide k step a wave reads 8 activation and 8 weight fragments for 64
-// MFMAs, two thirds of the 128 x 128 kernel's LDS reads per MFMA (12 for 32),
-// and a workgroup stores 32 KiB into LDS for twice the products of the 24
-// KiB the narrow kernel stores.
-constexpr int kTileWide = 256;
-constexpr int kWideElems = kTileWide * kTileK;  // one weight stage: 256 rows x 32 k
+// compute unit two): projection_gemm_wide_kernel<NW>, 128 x NW output tiles
+// (NW = 256, or 192 where 192-column tiles fill their rounds of two
+// workgroups per compute unit with fewer columns: gate|up at N=4096), 4 waves
+// of 64 x NW/2 (4 x NW/32 MFMA tiles, hi and lo), K in steps of 32.  The
+// activation stages (16 KiB) move through a three-stage ring, loaded two
+// steps ahead, the weight stages (NW x 64 bytes) through a two-stage ring,
+// loaded one step ahead: 80 (72) KiB, two workgroups per compute unit.  Per
+// 32-wide k step a wave reads 8 activation and NW/32 weight fragments for
+// NW/2 MFMAs, at NW = 256 two thirds of the 128 x 128 kernel's LDS reads per
+// MFMA (12 for 32), and a workgroup stores 32 KiB into LDS for twice the
+// products of the 24 KiB the narrow kernel stores.
 constexpr uint32_t kWideResident = 64;          // workgroups one XCD runs at once (32 compute units x 2)
 
 // Tile order of the wide GEMM.  Workgroup b runs on XCD b % 8, so XCD x
@@ -425,17 +425,22 @@ __device__ inline bool wide_tile(const WideOrder &o, uint32_t b, uint32_t *mt, u
     return true;
 }
 
+template <int NW>
 __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_wide_kernel(
     const uint16_t *__restrict__ tiles, const int32_t *__restrict__ exponents, const uint16_t *__restrict__ weight,
     const float *__restrict__ bias, float *__restrict__ out, uint32_t rows, uint32_t k_width, uint32_t n_width,
     WideOrder order) {
+    static_assert(NW == 256 || NW == 192, "wide column tile of 256 or 192");
+    constexpr int CB = NW / 32;    // 16-column MFMA tiles per wave
+    constexpr int kWL = NW / 64;   // weight loads (16 rows each) per wave and stage
+    constexpr int kWideElems = NW * kTileK;  // one weight stage: NW rows x 32 k
     uint32_t mt, nt;
     if (!wide_tile(order, blockIdx.x, &mt, &nt)) return;  // uniform: a smaller block of this XCD
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int row16 = lane & 15, kg = lane >> 4;
-    const uint32_t m0 = mt * kTileM, n0 = nt * kTileWide;
-    const int wm = wave >> 1, wn = wave & 1;  // the wave's 64 x 128 part: rows wm * 64, columns wn * 128
+    const uint32_t m0 = mt * kTileM, n0 = nt * NW;
+    const int wm = wave >> 1, wn = wave & 1;  // the wave's 64 x NW/2 part: rows wm * 64, columns wn * NW/2
     const uint32_t steps = k_width / kTileK;
 
     // The stages as distinct arrays, picked at compile time by the loop
@@ -445,16 +450,19 @@ __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_wide_kernel(
     typedef __attribute__((address_space(3))) void *lds_ptr;
 
     // Direct global-to-LDS loads, 1 KiB per instruction: activations as in
-    // the narrow kernel (4 per wave); weights 16 instructions of 16 rows, 4
-    // per wave, lane l of instruction j filling LDS slot p = 64 j + l (row p /
-    // 4, slot p % 4, the row's k-chunk slot ^ ((row / 2) % 4)).  Weight rows
-    // past the end re-read the last row (never stored).
+    // the narrow kernel (4 per wave); weights NW / 16 instructions of 16 rows,
+    // NW / 64 per wave, lane l of instruction j filling LDS slot p = 64 j + l
+    // (row p / 4, slot p % 4, the row's k-chunk slot ^ ((row / 2) % 4)).
+    // Weight rows past the end re-read the last row (never stored).
     const uint16_t *a_tiles = tiles + static_cast<size_t>(mt) * steps * kBlockElems + (wave * 4) * 512 + lane * 8;
     const uint32_t last_col = n_width - 1;
+    // (The per-thread arrays here have fixed sizes, the largest width's, and
+    // only their first kWL / CB entries are used: arrays whose size depends on
+    // the template argument make hipcc's host pass drop the launch stub.)
     size_t w_row_off[4];
 #pragma unroll
-    for (int rw = 0; rw < 4; ++rw) {
-        const int p = 64 * (wave * 4 + rw) + lane, wrow = p >> 2;
+    for (int rw = 0; rw < kWL; ++rw) {
+        const int p = 64 * (wave * kWL + rw) + lane, wrow = p >> 2;
         const int kc = (p & 3) ^ ((wrow >> 1) & 3);
         w_row_off[rw] = static_cast<size_t>(min(n0 + wrow, last_col)) * k_width + kc * 8;
     }
@@ -466,52 +474,53 @@ __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_wide_kernel(
     };
     auto load_w = [&](uint32_t s, uint16_t *dw) {
 #pragma unroll
-        for (int rw = 0; rw < 4; ++rw)
+        for (int rw = 0; rw < kWL; ++rw)
             __builtin_amdgcn_global_load_lds(weight + w_row_off[rw] + s * kTileK,
-                                             (lds_ptr)(dw + (wave * 4 + rw) * 512), 16, 0, 0);
+                                             (lds_ptr)(dw + (wave * kWL + rw) * 512), 16, 0, 0);
     };
 
     float4_t acc[4][8];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 8; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < CB; ++b) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     // The fragment layouts of the narrow kernel: A = activations (lane row
     // l % 16, k (l / 16) * 8 ..), B = W^T (lane column l % 16, same k).
     auto compute = [&](const uint16_t *sa, const uint16_t *sw) {
         half8_t bf[8];
 #pragma unroll
-        for (int cb = 0; cb < 8; ++cb)
-            bf[cb] = *reinterpret_cast<const half8_t *>(sw + w_offset(kg, wn * 128 + cb * 16 + row16));
+        for (int cb = 0; cb < CB; ++cb)
+            bf[cb] = *reinterpret_cast<const half8_t *>(sw + w_offset(kg, wn * (NW / 2) + cb * 16 + row16));
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             const int trow = wm * 64 + rb * 16 + row16;
             const half8_t ah = *reinterpret_cast<const half8_t *>(sa + a_offset(kg, trow));
             const half8_t al = *reinterpret_cast<const half8_t *>(sa + kTileElems + a_offset(kg, trow));
 #pragma unroll
-            for (int cb = 0; cb < 8; ++cb)
+            for (int cb = 0; cb < CB; ++cb)
                 acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bf[cb], acc[rb][cb], 0, 0, 0);
 #pragma unroll
-            for (int cb = 0; cb < 8; ++cb)
+            for (int cb = 0; cb < CB; ++cb)
                 acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[cb], acc[rb][cb], 0, 0, 0);
         }
         // Schedule: the weight fragments and the first row block's first,
-        // then each row block's 16 MFMAs with the next row block's two
-        // fragment reads issued after its first MFMA and the step's 8
+        // then each row block's 2 CB MFMAs with the next row block's two
+        // fragment reads issued after its first MFMA and the step's 4 + NW / 64
         // global-to-LDS loads spread among them (masks: 0x100 LDS read,
         // 0x008 MFMA, 0x020 global load).  Measured against the compiler's own
         // order (a wait for each row block's reads): gate|up 138 -> 127 us.
-        __builtin_amdgcn_sched_group_barrier(0x100, 10, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, CB + 2, 0);
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             if (rb < 3) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
             for (int q = 0; q < 3; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 5, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, (2 * CB - 1) / 3, 0);
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             }
+            if constexpr ((2 * CB - 1) % 3 != 0) __builtin_amdgcn_sched_group_barrier(0x008, (2 * CB - 1) % 3, 0);
         }
     };
     // Step s: wait until at most the 4 activation loads of stage s + 1 are
@@ -557,8 +566,8 @@ __global__ __launch_bounds__(kGemmThreads, 2) void projection_gemm_wide_kernel(
             if (r >= rows) continue;
             const int e = exponents[r];
 #pragma unroll
-            for (int cb = 0; cb < 8; ++cb) {
-                const uint32_t n = n0 + wn * 128 + cb * 16 + row16;
+            for (int cb = 0; cb < CB; ++cb) {
+                const uint32_t n = n0 + wn * (NW / 2) + cb * 16 + row16;
                 if (n < n_width) out[static_cast<size_t>(r) * n_width + n] = __builtin_ldexpf(acc[rb][cb][i], e) + bias[n];
             }
         }
@@ -600,17 +609,29 @@ int launch_linear_projection_f16(const float *input, const uint16_t *weight, con
     default: hipLaunchKernelGGL(projection_split_kernel<0>, split_grid, dim3(kSplitThreads), 0, st, input, rows, k_width, ws.tiles, ws.exponents); break;
     }
     if (hipError_t e = hipGetLastError()) return static_cast<int>(e);
-    const uint32_t wide_cols = n_width / kTileWide + (n_width % kTileWide != 0);
-    if (static_cast<uint64_t>(wide_cols) * m_tiles >= 2 * kTargetWorkgroups) {
+    const uint32_t cols256 = n_width / 256 + (n_width % 256 != 0), cols192 = n_width / 192 + (n_width % 192 != 0);
+    const uint64_t slots = 2 * kTargetWorkgroups;
+    if (static_cast<uint64_t>(cols256) * m_tiles >= slots) {
         // Enough wide tiles for two workgroups on every compute unit: the
         // wide kernel (with fewer, its second slot on most compute units
         // stays empty, and the narrow kernel's twice as many tiles finish
         // sooner: q|k|v at N=4096, 320 wide tiles, 80 us against 72).
+        // 192-column tiles where their rounds of two workgroups per compute
+        // unit hold fewer columns than the 256-column tiles' (gate|up at
+        // N=4096: 1024 tiles in two full rounds, against 768 tiles that leave
+        // the second round half empty).
+        const uint64_t rounds256 = (cols256 * m_tiles + slots - 1) / slots, rounds192 = (cols192 * m_tiles + slots - 1) / slots;
+        const bool narrow192 = rounds192 * 192 < rounds256 * 256;
+        const uint32_t wide_cols = narrow192 ? cols192 : cols256;
         const WideOrder order = wide_order(m_tiles, wide_cols);
         const uint32_t row_groups = kXcds / order.col_groups;
         const uint32_t block = ((m_tiles + row_groups - 1) / row_groups) * ((wide_cols + order.col_groups - 1) / order.col_groups);
-        hipLaunchKernelGGL(projection_gemm_wide_kernel, dim3(kXcds * block), dim3(kGemmThreads), 0, st, ws.tiles,
-                           ws.exponents, weight, bias, out, rows, k_width, n_width, order);
+        if (narrow192)
+            hipLaunchKernelGGL(projection_gemm_wide_kernel<192>, dim3(kXcds * block), dim3(kGemmThreads), 0, st,
+                               ws.tiles, ws.exponents, weight, bias, out, rows, k_width, n_width, order);
+        else
+            hipLaunchKernelGGL(projection_gemm_wide_kernel<256>, dim3(kXcds * block), dim3(kGemmThreads), 0, st,
+                               ws.tiles, ws.exponents, weight, bias, out, rows, k_width, n_width, order);
         return static_cast<int>(hipGetLastError());
     }
     const uint32_t tiles = (n_width / kTileN + (n_width % kTileN != 0)) * m_tiles;  // < 2^24 (checked by the caller)

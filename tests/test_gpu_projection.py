@@ -99,13 +99,16 @@ def test_rows_far_outside_the_fp16_range_keep_f32_accuracy():
     np.testing.assert_array_equal(got[2], b)
 
 
-@pytest.mark.parametrize("rows,k,n", [(4096, 1024, 6144),   # gate|up at N=4096: 768 wide tiles, 2 generations per XCD
-                                      (2049, 256, 7940),    # ragged rows and columns: uneven XCD blocks
-                                      (1100, 96, 16384)])   # 3 k steps: the ring's tail without a full period
+@pytest.mark.parametrize("rows,k,n", [(4096, 1024, 6144),   # gate|up at N=4096: 1024 tiles of 128 x 192, two full rounds
+                                      (2049, 256, 7940),    # ragged rows and columns (192): uneven XCD blocks
+                                      (1100, 96, 16384),    # 3 k steps (192): the ring's tail without a full period
+                                      (2048, 128, 8192),    # 512 tiles of 128 x 256 in one round: 256 columns
+                                      (1999, 160, 8000)])   # ragged rows and columns, 5 k steps: 256 columns
 def test_wide_kernel_writes_every_tile(rows, k, n):
-    """Shapes with at least 512 tiles of 128 x 256 run the wide GEMM, whose tiles each XCD takes in one block of
-    the output: every output element is written (the output starts as NaN) and two rows of every 128-row tile
-    (its first and last) are within the f64 bound over all columns."""
+    """Shapes with at least 512 tiles of 128 x 256 run the wide GEMM, 128 x 192 or 128 x 256 tiles (whichever
+    needs fewer columns' worth of rounds of two workgroups per compute unit), whose tiles each XCD takes in one
+    block of the output: every output element is written (the output starts as NaN) and two rows of every
+    128-row tile (its first and last) are within the f64 bound over all columns."""
     import torch
     log(f"case: wide projection rows={rows} k={k} n={n}")
     seed = rows + k + n
