@@ -200,32 +200,38 @@ __device__ inline void store_f32(uint64_t base, uint32_t index, float value) {
 // launches).  Wave row i belongs to member m = the number of members that end
 // at or before it.  Every argument is used unconditionally (pointers picked
 // by masks, not branches), so they arrive in one batch of scalar loads rather
-// than a chain of dependent ones (a chain cost about 1 us per launch).
+// than a chain of dependent ones (a chain cost about 1 us per launch).  The
+// members come as separate arguments, weights, row ends, total and vector
+// first: those 14 dwords are preloaded into SGPRs at wave launch
+// (-amdgpu-kernarg-preload-count=16; a struct argument is not preloaded), so
+// the weight loads issue without a scalar-load round trip.
 template <int CHUNKS>
-__global__ __launch_bounds__(kGemvWaves * 64) void gemv_group_f16_kernel(GemvGroup g,
-                                                                           const float *__restrict__ vector) {
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_group_f16_kernel(
+    const uint16_t *w0, const uint16_t *w1, const uint16_t *w2, const uint16_t *w3, uint32_t end0, uint32_t end1,
+    uint32_t end2, uint32_t total, const float *__restrict__ vector, float *o0, float *o1, float *o2, float *o3) {
     constexpr int kColumns = CHUNKS * 512;
-    // The output pointers are read only by the storing lane at the end; named
-    // here, they arrive with the other arguments instead of in a scalar-load
-    // round trip of their own after the reduction.
-    asm volatile("" ::"s"(g.out[0]), "s"(g.out[1]), "s"(g.out[2]), "s"(g.out[3]));
     const int lane = threadIdx.x & 63;
     const uint32_t grow =
         static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * kGemvWaves + (threadIdx.x >> 6))));
-    const uint32_t rr = min(grow, g.total - 1);  // rows past the end re-read the last row, unstored
-    const uint32_t m = (rr >= g.end[0] ? 1u : 0u) + (rr >= g.end[1] ? 1u : 0u) + (rr >= g.end[2] ? 1u : 0u);
+    const uint32_t rr = min(grow, total - 1);  // rows past the end re-read the last row, unstored
+    const uint32_t m = (rr >= end0 ? 1u : 0u) + (rr >= end1 ? 1u : 0u) + (rr >= end2 ? 1u : 0u);
     auto pick = [m](uint64_t a0, uint64_t a1, uint64_t a2, uint64_t a3) {
         return (m == 0 ? a0 : 0ull) | (m == 1 ? a1 : 0ull) | (m == 2 ? a2 : 0ull) | (m == 3 ? a3 : 0ull);
     };
-    const uint64_t wbase = pick(reinterpret_cast<uint64_t>(g.weights[0]), reinterpret_cast<uint64_t>(g.weights[1]),
-                                reinterpret_cast<uint64_t>(g.weights[2]), reinterpret_cast<uint64_t>(g.weights[3]));
-    const uint64_t obase = pick(reinterpret_cast<uint64_t>(g.out[0]), reinterpret_cast<uint64_t>(g.out[1]),
-                                reinterpret_cast<uint64_t>(g.out[2]), reinterpret_cast<uint64_t>(g.out[3]));
-    const uint32_t begin = static_cast<uint32_t>(pick(0, g.end[0], g.end[1], g.end[2]));
+    const uint64_t wbase = pick(reinterpret_cast<uint64_t>(w0), reinterpret_cast<uint64_t>(w1),
+                                reinterpret_cast<uint64_t>(w2), reinterpret_cast<uint64_t>(w3));
+    const uint64_t obase = pick(reinterpret_cast<uint64_t>(o0), reinterpret_cast<uint64_t>(o1),
+                                reinterpret_cast<uint64_t>(o2), reinterpret_cast<uint64_t>(o3));
+    const uint32_t begin = static_cast<uint32_t>(pick(0, end0, end1, end2));
     const uint32_t row = rr - begin;
     half8_t w[CHUNKS];
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c) w[c] = load_half8_nt(wbase, static_cast<size_t>(row) * kColumns + (c * 64 + lane) * 8);
+    // The output pointers (not preloaded) are read only by the storing lane at
+    // the end; named here, behind the weight loads, their scalar load returns
+    // while the weights stream instead of in a round trip of its own after
+    // the reduction.
+    asm volatile("" ::"s"(o0), "s"(o1), "s"(o2), "s"(o3));
     float4_t x[CHUNKS][2];
     load_vector_lds<CHUNKS>(vector, x);
     float acc = 0.f;
@@ -234,7 +240,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_group_f16_kernel(GemvGro
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc = __builtin_fmaf(static_cast<float>(w[c][j]), x[c][j >> 2][j & 3], acc);
     acc = wave_sum(acc);
-    if (grow < g.total && lane == 0) store_f32(obase, row, acc);
+    if (grow < total && lane == 0) store_f32(obase, row, acc);
 }
 
 // Standalone top-1 over a logit row: a grid-stride scan in float4 lanes
@@ -311,12 +317,18 @@ int launch_top1_finish(Top1Slot *slots, uint32_t *result, hipStream_t st) {
 int launch_gemv_group_f16(const GemvGroup &group, const float *vector, uint32_t columns, void *stream) {
     hipStream_t st = static_cast<hipStream_t>(stream);
     const unsigned wgs = (group.total + kGemvWaves - 1) / kGemvWaves;
+    static_assert(kGemvGroupMax == 4, "four member slots");
+#define PVLC_GEMV_GROUP_LAUNCH(C)                                                                                   \
+    hipLaunchKernelGGL(gemv_group_f16_kernel<C>, dim3(wgs), dim3(kGemvWaves * 64), 0, st, group.weights[0],        \
+                       group.weights[1], group.weights[2], group.weights[3], group.end[0], group.end[1], group.end[2], \
+                       group.total, vector, group.out[0], group.out[1], group.out[2], group.out[3])
     switch (columns) {
-        case 1024: hipLaunchKernelGGL(gemv_group_f16_kernel<2>, dim3(wgs), dim3(kGemvWaves * 64), 0, st, group, vector); break;
-        case 2048: hipLaunchKernelGGL(gemv_group_f16_kernel<4>, dim3(wgs), dim3(kGemvWaves * 64), 0, st, group, vector); break;
-        case 3072: hipLaunchKernelGGL(gemv_group_f16_kernel<6>, dim3(wgs), dim3(kGemvWaves * 64), 0, st, group, vector); break;
+        case 1024: PVLC_GEMV_GROUP_LAUNCH(2); break;
+        case 2048: PVLC_GEMV_GROUP_LAUNCH(4); break;
+        case 3072: PVLC_GEMV_GROUP_LAUNCH(6); break;
         default: return static_cast<int>(hipErrorInvalidValue);
     }
+#undef PVLC_GEMV_GROUP_LAUNCH
     return static_cast<int>(hipGetLastError());
 }
 
