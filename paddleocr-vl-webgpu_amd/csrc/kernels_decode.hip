@@ -103,33 +103,43 @@ __device__ inline uint32_t wave_tile_ids(const DecodeParams &p, uint32_t s, int 
 // measured 11% and 8% faster with them, the 18-layer step 2% (a step whose
 // cache already sits in the Infinity Cache is slower, 11.1 -> 11.8 us).
 template <int PAIRS>
-__device__ inline void load_chunk(const DecodeParams &p, uint32_t g, uint32_t ids, int c, int row, int kg,
-                                  half8_t (&kr)[PAIRS][2][4], half8_t (&vr)[PAIRS][8]) {
-    const uint16_t *kbase[PAIRS];
-    const uint16_t *vbase[PAIRS];
+__device__ inline void load_chunk_keys(const DecodeParams &p, uint32_t g, uint32_t ids, int c, int row, int kg,
+                                       half8_t (&kr)[PAIRS][2][4]) {
 #pragma unroll
     for (int j = 0; j < PAIRS; ++j) {
         const int t0 = c * 2 * PAIRS + 2 * j;
         const size_t b0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ids), t0));
         const size_t b1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ids), t0 + 1));
-        kbase[j] = p.key_cache + ((row < 8 ? b0 : b1) * kKvHeads + g) * kBlockHeadElems;
-        vbase[j] = p.value_cache + ((kg < 2 ? b0 : b1) * kKvHeads + g) * kBlockHeadElems;
-    }
-#pragma unroll
-    for (int j = 0; j < PAIRS; ++j)
+        const uint16_t *kbase = p.key_cache + ((row < 8 ? b0 : b1) * kKvHeads + g) * kBlockHeadElems;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb)
                 kr[j][h][kb] = __builtin_nontemporal_load(
-                    reinterpret_cast<const half8_t *>(kbase[j] + (kb * 4 + kg) * 128 + (h * 8 + (row & 7)) * 8));
-    __builtin_amdgcn_sched_barrier(0);  // keep every key load ahead of the value loads
+                    reinterpret_cast<const half8_t *>(kbase + (kb * 4 + kg) * 128 + (h * 8 + (row & 7)) * 8));
+    }
+}
+template <int PAIRS>
+__device__ inline void load_chunk_values(const DecodeParams &p, uint32_t g, uint32_t ids, int c, int row, int kg,
+                                         half8_t (&vr)[PAIRS][8]) {
 #pragma unroll
-    for (int j = 0; j < PAIRS; ++j)
+    for (int j = 0; j < PAIRS; ++j) {
+        const int t0 = c * 2 * PAIRS + 2 * j;
+        const size_t b0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ids), t0));
+        const size_t b1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ids), t0 + 1));
+        const uint16_t *vbase = p.value_cache + ((kg < 2 ? b0 : b1) * kKvHeads + g) * kBlockHeadElems;
 #pragma unroll
         for (int cc = 0; cc < 8; ++cc)
             vr[j][cc] = __builtin_nontemporal_load(
-                reinterpret_cast<const half8_t *>(vbase[j] + (cc * 16 + row) * 16 + (kg & 1) * 8));
+                reinterpret_cast<const half8_t *>(vbase + (cc * 16 + row) * 16 + (kg & 1) * 8));
+    }
+}
+template <int PAIRS>
+__device__ inline void load_chunk(const DecodeParams &p, uint32_t g, uint32_t ids, int c, int row, int kg,
+                                  half8_t (&kr)[PAIRS][2][4], half8_t (&vr)[PAIRS][8]) {
+    load_chunk_keys<PAIRS>(p, g, ids, c, row, kg, kr);
+    __builtin_amdgcn_sched_barrier(0);  // keep every key load ahead of the value loads
+    load_chunk_values<PAIRS>(p, g, ids, c, row, kg, vr);
 }
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -144,16 +154,18 @@ __device__ inline void load_pair_sc1(const float *q, float *lo, float *hi) {
 }
 
 // One work item: partition `part` of kv head g of sequence s, whose cache
-// holds cache_len rows before the append (rotary position pos); ids are the
+// holds cache_len rows before the append (rotary position pos, or, with
+// pos_from_params, p.positions[s] -- cache_len without positions -- read
+// behind the first key loads); ids are the
 // wave's tile block ids (wave_tile_ids) and ids_bad whether one of them was
 // out of range.  With DEFER_MERGE the partial is only stored (plain stores)
 // for paged_decode_merge_kernel, launched after this kernel; otherwise the
 // last partition to arrive merges all partitions in-kernel.  Every return is
 // uniform over the workgroup.  Errors are reported after the key/value loads
 // are consumed, so no conditional memory operation sits among them.
-template <int WAVES, int PAIRS, bool DEFER_MERGE, bool F32IO>
+template <int WAVES, int PAIRS, bool DEFER_MERGE, bool F32IO, bool KEYS_FIRST = true>
 __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uint32_t g, uint32_t part, int cache_len,
-                                   int pos, uint32_t ids, bool ids_bad) {
+                                   int pos, uint32_t ids, bool ids_bad, bool pos_from_params = false) {
     constexpr int kChunkTiles = 2 * PAIRS;         // 16-token tiles a wave holds in registers at once
     constexpr int kChunkTokens = kChunkTiles * 16;
     const int lane = threadIdx.x & 63;
@@ -168,82 +180,118 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     const int part_end = min(part_start + P, T);
     const int num_parts = (T + P - 1) / P;
 
+    // KEYS_FIRST: the first chunk's keys go out first -- their addresses need
+    // only the arguments the single-shot kernel takes preloaded in SGPRs, so
+    // the key stream starts without waiting for a scalar load -- then the
+    // small operands (their pointers' scalar loads return while the keys
+    // stream), then the values; the query and rotary rows are waited for with
+    // the keys, which the scores need first anyway (config 2: 11.67-11.69 ->
+    // 11.44-11.46 us).  Without it (a launch that rotates the query) the small
+    // operands go first, so the rotation runs while the keys and values are
+    // in flight instead of after the keys arrive (single-layer f32-operand
+    // decode: 7.71-7.74 us, against 8.18-8.21 with the keys first).  (Waves
+    // past the end of a short partition re-read the partition's last tile and
+    // never use it.)
+    half8_t kr[PAIRS][2][4];
+    half8_t vr[PAIRS][8];
+    int ws = part_start + wave * kChunkTokens;
+    if constexpr (KEYS_FIRST) {
+        load_chunk_keys<PAIRS>(p, g, ids, 0, row, kg, kr);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Every pointer the small operands and the prologue need, named here so
+    // they arrive in one round of scalar loads (left to itself the compiler
+    // loads each where it is first needed, behind branches on the optional
+    // ones: four dependent rounds).
+    asm volatile("" ::"s"(p.positions), "s"(p.rope_cos), "s"(p.rope_sin), "s"(p.rope_rows));
+    if constexpr (F32IO) asm volatile("" ::"s"(p.query32), "s"(p.new_key32), "s"(p.new_value32));
+    else asm volatile("" ::"s"(p.query), "s"(p.new_key), "s"(p.new_value));
+
     // Rotary position of the appended row (and of the query).
+    if (pos_from_params) pos = p.positions ? load_const(p.positions, s) : cache_len;
     bool rope = p.rope_cos != nullptr;
     const bool rope_bad = rope && (pos < 0 || static_cast<uint32_t>(pos) >= p.rope_rows);
     if (rope_bad) rope = false;
     const float *cos_row = rope ? p.rope_cos + static_cast<size_t>(pos) * 64 : nullptr;
     const float *sin_row = rope ? p.rope_sin + static_cast<size_t>(pos) * 64 : nullptr;
 
-    // Small operands are loaded first and before the key/value stream, so
-    // they return ahead of it and every later wait on them is a partial one.
-    // The query is the B operand of the score MFMA: column = query head of
-    // the group (8 real, 8 zero), k = dims kb*32 + kg*8 .. +8 (with fp16
-    // operands the lanes of the zero columns load a real row and discard it).
-    // With f32 operands the query is kept as given until it is rotated, and
-    // rounded to fp16 once (RNE), as the new key below.
     const size_t qoff = (static_cast<size_t>(s) * kQueryHeads + g * kGroup + (row & 7)) * kHeadDim;
+    const size_t new_base = (static_cast<size_t>(s) * kKvHeads + g) * kHeadDim;
+    // (Without rotary the cos/sin loads read the new key row as a stand-in,
+    // so they stay unconditional; the values are then replaced by cos 1,
+    // sin 0.)
+    const float *stand_in = F32IO ? p.new_key32 + new_base : reinterpret_cast<const float *>(p.new_key + new_base);
+    const float *cos_src = rope ? cos_row : stand_in;
+    const float *sin_src = rope ? sin_row : stand_in;
+    // Raw loads first, every lane, then the first chunk's values, and only
+    // then any arithmetic on the small operands: a conversion between them
+    // made the compiler wait for the keys before issuing the values.  With f32
+    // operands the zero columns' lanes read the rows of columns 0-7 again (the
+    // same cache lines) and are selected away afterwards; loads on only some
+    // lanes, behind the key loads, also forced that wait (single-layer decode
+    // 7.80 -> 8.22 us).
     half8_t qb[4];
-    float qf[F32IO ? 4 : 1][8];
+    float4_t q32[F32IO ? 4 : 1][2];
+    float nkf_lo = 0.f, nkf_hi = 0.f, nvf_lo = 0.f, nvf_hi = 0.f;  // f32 operands: the new row as given
+    uint16_t nk_lo = 0, nk_hi = 0, nv_lo = 0, nv_hi = 0;
     if constexpr (F32IO) {
-        // Only the lanes of the 8 real columns load the f32 query (8 KiB a
-        // wave otherwise, twice what the columns use: single-layer decode
-        // 7.98 -> 7.85 us; the fp16 query, half the bytes, stays unmasked,
-        // where masking measured 0.1 us slower on config 2).
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            float4_t lo = {0.f, 0.f, 0.f, 0.f}, hi = lo;
-            if (row < static_cast<int>(kGroup)) {
-                lo = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8);
-                hi = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8 + 4);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                qf[kb][j] = lo[j];
-                qf[kb][j + 4] = hi[j];
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qb[kb][j] = to_h(qf[kb][j]);
+            q32[kb][0] = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8);
+            q32[kb][1] = *reinterpret_cast<const float4_t *>(p.query32 + qoff + kb * 32 + kg * 8 + 4);
         }
+        nkf_lo = p.new_key32[new_base + lane];
+        nkf_hi = p.new_key32[new_base + lane + 64];
+        nvf_lo = p.new_value32[new_base + lane];
+        nvf_hi = p.new_value32[new_base + lane + 64];
     } else {
         const uint16_t *qrow = p.query + qoff;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) qb[kb] = *reinterpret_cast<const half8_t *>(qrow + kb * 32 + kg * 8);
-    }
-    // The appended row and the rotary row at its position: lane t holds
-    // dims t and t+64 (the rotate-half pair) and cos/sin of pair t.
-    const size_t new_base = (static_cast<size_t>(s) * kKvHeads + g) * kHeadDim;
-    uint16_t nk_lo, nk_hi, nv_lo, nv_hi;
-    float nkf_lo = 0.f, nkf_hi = 0.f;  // f32 operands: the new key before its rotation and rounding
-    if constexpr (F32IO) {
-        nkf_lo = p.new_key32[new_base + lane];
-        nkf_hi = p.new_key32[new_base + lane + 64];
-        nk_lo = __builtin_bit_cast(uint16_t, to_h(nkf_lo));
-        nk_hi = __builtin_bit_cast(uint16_t, to_h(nkf_hi));
-        nv_lo = __builtin_bit_cast(uint16_t, to_h(p.new_value32[new_base + lane]));
-        nv_hi = __builtin_bit_cast(uint16_t, to_h(p.new_value32[new_base + lane + 64]));
-    } else {
         nk_lo = p.new_key[new_base + lane];
         nk_hi = p.new_key[new_base + lane + 64];
         nv_lo = p.new_value[new_base + lane];
         nv_hi = p.new_value[new_base + lane + 64];
     }
-    // (Without rotary the loads read the new key row as a stand-in, so they
-    // stay unconditional; the values are then replaced by cos 1, sin 0.)
-    const float *stand_in = F32IO ? p.new_key32 + new_base : reinterpret_cast<const float *>(p.new_key + new_base);
-    const float *cos_src = rope ? cos_row : stand_in;
-    const float *sin_src = rope ? sin_row : stand_in;
     const float rc_raw = cos_src[lane];
     const float rs_raw = sin_src[lane];
+
+    // First chunk's keys (if not issued above) and values.
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!KEYS_FIRST) {
+        load_chunk_keys<PAIRS>(p, g, ids, 0, row, kg, kr);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    load_chunk_values<PAIRS>(p, g, ids, 0, row, kg, vr);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // The query is the B operand of the score MFMA: column = query head of
+    // the group (8 real, 8 zero), k = dims kb*32 + kg*8 .. +8 (with fp16
+    // operands the lanes of the zero columns load a real row and discard it).
+    // With f32 operands the query is kept as given until it is rotated, and
+    // rounded to fp16 once (RNE), as the new key below.  The appended row:
+    // lane t holds dims t and t+64 (the rotate-half pair) and cos/sin of pair
+    // t.
+    float qf[F32IO ? 4 : 1][8];
+    if constexpr (F32IO) {
+        const bool real = row < static_cast<int>(kGroup);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                qf[kb][j] = real ? q32[kb][0][j] : 0.f;
+                qf[kb][j + 4] = real ? q32[kb][1][j] : 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qb[kb][j] = to_h(qf[kb][j]);
+        }
+        nk_lo = __builtin_bit_cast(uint16_t, to_h(nkf_lo));
+        nk_hi = __builtin_bit_cast(uint16_t, to_h(nkf_hi));
+        nv_lo = __builtin_bit_cast(uint16_t, to_h(nvf_lo));
+        nv_hi = __builtin_bit_cast(uint16_t, to_h(nvf_hi));
+    }
     const float rc = rope ? rc_raw : 1.0f;
     const float rs = rope ? rs_raw : 0.0f;
-
-    // First chunk's keys and values (waves past the end of a short partition
-    // re-read the partition's last tile and never use it).
-    half8_t kr[PAIRS][2][4];
-    half8_t vr[PAIRS][8];
-    int ws = part_start + wave * kChunkTokens;
-    load_chunk<PAIRS>(p, g, ids, 0, row, kg, kr, vr);
 
     if (rope && p.rotate_query) {
         // Rotate-half of the query in place: the partner of chunk kb is
@@ -662,17 +710,25 @@ __device__ inline int64_t checked_cache_len(const DecodeParams &p, int64_t len) 
 
 // Grid (partition, kv head, sequence): sequences of one uniform length, or
 // ragged lengths when there are too many sequences for the ragged kernel.
-template <int WAVES, int PAIRS, bool F32IO>
-__global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParams p) {
-    // Every argument the prologue reads, loaded in one round of scalar loads:
-    // left to itself the compiler loads them where each is first needed, and
-    // the branches on the optional pointers made that four dependent rounds
-    // before the first key/value load (config 2: 11.91-11.94 -> 11.70-11.75 us).
-    asm volatile("" ::"s"(p.cache_lens), "s"(p.uniform_cache_len), "s"(p.block_tables), "s"(p.max_blocks_per_seq),
-                 "s"(p.num_blocks), "s"(p.partition_tokens), "s"(p.max_parts), "s"(p.positions), "s"(p.key_cache),
-                 "s"(p.value_cache), "s"(p.rope_cos), "s"(p.rope_sin), "s"(p.rope_rows));
-    if constexpr (F32IO) asm volatile("" ::"s"(p.query32), "s"(p.new_key32), "s"(p.new_value32));
-    else asm volatile("" ::"s"(p.query), "s"(p.new_key), "s"(p.new_value));
+// The arguments the first key loads' addresses depend on come ahead of the
+// parameter block, as scalars: the first 14 dwords of kernel arguments are
+// preloaded into SGPRs at wave launch (-amdgpu-kernarg-preload-count=16; a
+// struct argument is not), so the key stream starts without a scalar-load
+// round trip.  The copies in p are not read.
+template <int WAVES, int PAIRS, bool F32IO, bool KEYS_FIRST>
+__global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(
+    uint16_t *key_cache, uint16_t *value_cache, const int32_t *cache_lens, const int32_t *block_tables,
+    uint32_t uniform_cache_len, uint32_t max_blocks_per_seq, uint32_t num_blocks, uint32_t partition_tokens,
+    uint32_t max_parts, DecodeParams p) {
+    p.key_cache = key_cache;
+    p.value_cache = value_cache;
+    p.cache_lens = cache_lens;
+    p.block_tables = block_tables;
+    p.uniform_cache_len = uniform_cache_len;
+    p.max_blocks_per_seq = max_blocks_per_seq;
+    p.num_blocks = num_blocks;
+    p.partition_tokens = partition_tokens;
+    p.max_parts = max_parts;
     const uint32_t part = blockIdx.x;
     const uint32_t g = blockIdx.y;  // kv head
     const uint32_t s = blockIdx.z;  // sequence (or layer)
@@ -690,9 +746,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void paged_decode_kernel(DecodeParam
     bool bad = false;
     const uint32_t ids =
         wave_tile_ids<WAVES, 2 * PAIRS>(p, s, part_start, min(part_start + P, cache_len + 1), wave, &bad);
-    const int pos = p.positions ? load_const(p.positions, s) : cache_len;
-    decode_item<WAVES, PAIRS, false, F32IO>(p, static_cast<int>(p.partition_tokens), s, g, part, cache_len, pos, ids,
-                                            bad);
+    decode_item<WAVES, PAIRS, false, F32IO, KEYS_FIRST>(p, static_cast<int>(p.partition_tokens), s, g, part,
+                                                        cache_len, 0, ids, bad, /*pos_from_params=*/true);
 }
 
 // Exclusive scan of one int per thread over the workgroup; *total receives
@@ -990,8 +1045,17 @@ int launch_paged_decode_kernels(const DecodeLaunch &launch, DecodeParams &p, hip
     // Single-shot regime: one workgroup per (partition, kv head, sequence);
     // the last partition to arrive merges.
     const dim3 grid(launch.max_parts, kKvHeads, a.num_seqs);
-#define PVLC_DECODE_LAUNCH(W, PR) \
-    hipLaunchKernelGGL((paged_decode_kernel<W, PR, F32IO>), grid, dim3((W) * 64), 0, st, p)
+#define PVLC_DECODE_LAUNCH(W, PR)                                                                               \
+    do {                                                                                                        \
+        if (p.rotate_query)                                                                                     \
+            hipLaunchKernelGGL((paged_decode_kernel<W, PR, F32IO, false>), grid, dim3((W) * 64), 0, st,         \
+                               p.key_cache, p.value_cache, p.cache_lens, p.block_tables, p.uniform_cache_len,   \
+                               p.max_blocks_per_seq, p.num_blocks, p.partition_tokens, p.max_parts, p);         \
+        else                                                                                                    \
+            hipLaunchKernelGGL((paged_decode_kernel<W, PR, F32IO, true>), grid, dim3((W) * 64), 0, st,          \
+                               p.key_cache, p.value_cache, p.cache_lens, p.block_tables, p.uniform_cache_len,   \
+                               p.max_blocks_per_seq, p.num_blocks, p.partition_tokens, p.max_parts, p);         \
+    } while (0)
     switch (launch.waves) {
         case 1: PVLC_DECODE_LAUNCH(1, 1); break;
         case 2: PVLC_DECODE_LAUNCH(2, 1); break;
