@@ -15,9 +15,11 @@
 // LDS; the partitions of a (sequence, kv head) count their arrivals on a
 // device-scope counter, and the last to arrive merges all partitions.
 //
-// Latency discipline (the whole step is a few microseconds): every wave
-// issues its first chunk's loads before anything else; block ids come from
-// scalar loads; the appended row is rotated with vector loads while those
+// Latency discipline (the whole step is a few microseconds): the arguments
+// the first key loads need arrive preloaded in SGPRs, so every wave issues
+// its first chunk's keys before anything else (unless it rotates the query,
+// whose operands then go first); block ids come from one vector load per
+// wave (or arithmetic); the appended row is rotated while the key and value
 // loads are in flight; the merge loads partials in batches.
 //
 // Reference behaviour replaced: decoder_kv_append_f32, decoder_mrope_f32 (k
