@@ -526,19 +526,30 @@ __device__ inline void decode_item(const DecodeParams &p, int P, uint32_t s, uin
     const bool active = threadIdx.x < kCT;
     const int e0 = active ? static_cast<int>(threadIdx.x) * kPer : 0;
     const int h = e0 >> 7, d0 = e0 & 127;
+    // Every wave's (m, l, o) read first, in one batch: folded as they were
+    // read, the reads went out one or two at a time, each behind a wait.
+    float mw[WAVES], lw[WAVES], ow[WAVES][kPer];
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+        mw[w] = sm_m[w][h];
+        lw[w] = sm_l[w][h];
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) ow[w][e] = sm_o[w][h][d0 + e];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, sm_m[w][h]);
+    for (int w = 0; w < WAVES; ++w) M = fmaxf(M, mw[w]);
     float L = 0.f;
     float po[kPer];
 #pragma unroll
     for (int e = 0; e < kPer; ++e) po[e] = 0.f;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) {
-        const float f = __builtin_amdgcn_exp2f(sm_m[w][h] - M);  // 0 for a wave without tokens
-        L += sm_l[w][h] * f;
+        const float f = __builtin_amdgcn_exp2f(mw[w] - M);  // 0 for a wave without tokens
+        L += lw[w] * f;
 #pragma unroll
-        for (int e = 0; e < kPer; ++e) po[e] += sm_o[w][h][d0 + e] * f;
+        for (int e = 0; e < kPer; ++e) po[e] += ow[w][e] * f;
     }
 
     // Output element i of this (sequence, kv head): fp16 (RNE) or f32.
