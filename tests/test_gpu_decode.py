@@ -558,6 +558,15 @@ def test_paged_long_context_split_k():
     paged_case(8, 1024, 9000, seed=950, partition=512, log_uniform=True)
 
 
+@pytest.mark.parametrize("partition", [0, 32])
+def test_more_ragged_sequences_than_the_persistent_kernel_numbers(partition):
+    """A ragged batch of 2049 sequences, one more than the persistent kernel numbers in LDS, runs one workgroup
+    per (partition, kv head, sequence) at the planned partition, with each sequence's own length and the
+    in-kernel merge.  Every sequence's cache rows are checked bit-exact and its attention against the oracle."""
+    log(f"case: 2049 ragged seqs T in [1, 48], partition={partition}")
+    paged_case(2049, 1, 48, seed=880 + partition, partition=partition)
+
+
 def test_one_workspace_across_launch_paths_and_partitions():
     # The split-K merge relies on the workspace's sentinels; every launch must restore them, whichever path
     # (single-shot in-kernel merge or streaming partials + merge kernel) and partition stride it used.
