@@ -122,6 +122,21 @@ def test_split_schedule_matches_the_oracle(n):
     sampled_rows_match_decode(out, qr, kr, vr, n, rows, f"split N={n}")
 
 
+def test_split_schedule_through_a_permuted_block_table():
+    """The split-K pair schedule (a workspace, N > 2048) over a permuted block table with spare blocks and a
+    ragged last block: cache rows through the table bit-exact, sampled rows on both sides of the split point
+    against decode over i + 1 keys."""
+    n, nb = 2500, 200
+    log(f"case: split prefill through a permuted block table, N={n}, {nb} blocks")
+    rng = np.random.default_rng(11)
+    table = rng.permutation(nb)[:(n + 15) // 16].astype(np.int32)
+    ws = prefill_workspace(n)
+    assert ws[1] > 0
+    out, qr, kr, vr, scratch, q = run_prefill(n, seed=2500, table=table, num_blocks=nb, workspace=ws)
+    rows = [0, 15, 16, 1023, 1024, 2047, 2048, 2049, 2300, n - 17, n - 2, n - 1]
+    sampled_rows_match_decode(out, qr, kr, vr, n, rows, f"split N={n} permuted table")
+
+
 def test_split_and_unsplit_schedules_agree_and_the_workspace_is_reusable():
     import torch
     n = 4096
