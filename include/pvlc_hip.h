@@ -377,7 +377,9 @@ typedef struct pvlc_hip_paged_decode_args {
  * and at most 4096 tokens, so the items spread evenly over the compute units;
  * it records the partition it used in the workspace word after the error word
  * (pvlc_hip_paged_decode_streaming_partition gives the same choice on the
- * host). */
+ * host).  Ragged batches of more than 2048 sequences (more than the streaming
+ * kernel numbers) run one workgroup per (partition, kv head, sequence) at
+ * this partition instead, with the in-kernel merge. */
 uint32_t pvlc_hip_paged_decode_partition(uint32_t num_seqs, uint32_t max_context);
 /* The partition an automatic launch over these ragged cache lengths (rows
  * cached before the append; host memory, num_seqs entries) settles on, on a
